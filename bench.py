@@ -1,0 +1,207 @@
+"""Benchmark of the gfx950 attention hot path (one GPU).
+
+Workload: paged bf16 decode attention plus the K/V
+store of the new token: batch 64, 16 q / 8 kv heads, head_dim 128, per-request
+KV length uniform in [512, 4096], page size 1, page table a seeded random
+permutation of a 4M-slot pool, Q/K/V ~ N(0,1), sm_scale 1/sqrt(128), one new
+token's K/V written per request via int64 positions.
+
+A step = write_kv(64 new tokens) + decode attention for one layer, on a plan
+prepared once per forward (as the reference reuses one plan across layers).
+`value` = algorithmic bytes of a step / measured step time. The roofline
+object is for the decode kernels alone, timed with HIP events on the stream
+they run on.
+
+Prints ONE JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode-attn HBM GB/s (% peak); prefill MFMA util; output tok/s Qwen3-8B"
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--seed", type=int, default=2)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-requests", type=int, default=16,
+                   help="requests in the bounded CPU-baseline sample")
+    return p.parse_args()
+
+
+def build_workload(seed: int, dev: torch.device):
+    B, HQ, HKV, D, POOL = 64, 16, 8, 128, 1 << 22
+    g = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(512, 4097, (B,), generator=g, dtype=torch.int32)
+    perm = torch.randperm(POOL - 1, generator=g)[: int(lengths.sum())] + 1  # slot 0 reserved
+    cols = 4096
+    table = torch.zeros(B, cols, dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        n = int(lengths[b])
+        table[b, :n] = perm[off: off + n].to(torch.int32)
+        off += n
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    kc = torch.randn(POOL, 1, HKV, D, generator=gd, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn(POOL, 1, HKV, D, generator=gd, device=dev, dtype=torch.bfloat16)
+    kc[0].zero_()
+    vc[0].zero_()
+    q = torch.randn(B, HQ, D, generator=gd, device=dev, dtype=torch.bfloat16)
+    knew = torch.randn(B, HKV, D, generator=gd, device=dev, dtype=torch.bfloat16)
+    vnew = torch.randn(B, HKV, D, generator=gd, device=dev, dtype=torch.bfloat16)
+    loc = torch.tensor([int(table[b, int(lengths[b]) - 1]) for b in range(B)],
+                       dtype=torch.int64, device=dev)
+    return dict(B=B, HQ=HQ, HKV=HKV, D=D, POOL=POOL, lengths=lengths, table=table, kc=kc, vc=vc,
+                q=q, knew=knew, vnew=vnew, loc=loc)
+
+
+def decode_bytes(lengths, hq, hkv, d) -> int:
+    total = int(lengths.sum())
+    b = lengths.numel()
+    return total * hkv * d * 2 * 2 + total * 4 + b * hq * d * 2 * 2
+
+
+def store_bytes(b, hkv, d) -> int:
+    return b * (hkv * d * 2 * 2 + hkv * d * 2 * 2) + b * 8
+
+
+def cpu_baseline(w, requests: int):
+    """Oracle's torch-CPU fp32 restatement of the reference decode path on a sample."""
+    from oracle import attention as oatt
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    idx = list(range(requests))
+    lens = [int(w["lengths"][i]) for i in idx]
+    # Compact CPU pool holding only the sampled requests' slots (same gather pattern).
+    slots = torch.cat([w["table"][i, :lens[i]].long() for i in idx])
+    kc = w["kc"].view(w["POOL"], -1)[slots.to(w["kc"].device)].float().cpu()
+    vc = w["vc"].view(w["POOL"], -1)[slots.to(w["vc"].device)].float().cpu()
+    kc = kc.view(-1, 1, w["HKV"], w["D"])
+    vc = vc.view(-1, 1, w["HKV"], w["D"])
+    table = torch.zeros(len(idx), max(lens), dtype=torch.int32)
+    off = 0
+    for r, n in enumerate(lens):
+        table[r, :n] = torch.arange(off, off + n, dtype=torch.int32)
+        off += n
+    q = w["q"][idx].float().cpu()
+    oatt.decode_with_cache_torch(q, kc, vc, table, lens, 1)  # warm-up
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        oatt.decode_with_cache_torch(q, kc, vc, table, lens, 1)
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    nbytes = decode_bytes(torch.tensor(lens), w["HQ"], w["HKV"], w["D"])
+    return {"value": nbytes / sec / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{len(idx)} of 64 requests ({sum(lens)} KV tokens), libtorch fp32 CPU "
+                      "decode_with_cache restatement, median of 5"}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
+        sys.exit(2)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from llm_infer_rust_amd.backend import (AttentionMetadata, AttentionSpec, BatchPhase,
+                                            prepare_decode_plan, run_decode)
+    from llm_infer_rust_amd.kv_cache import BaseAttention
+
+    dev = torch.device("cuda", 0)
+    w = build_workload(args.seed, dev)
+    B, HQ, HKV, D = w["B"], w["HQ"], w["HKV"], w["D"]
+    cache = BaseAttention()
+    cache.set_reserved_write_slot(0)
+    cache.bind_kv_cache(w["kc"], w["vc"])
+    spec = AttentionSpec(HQ, HKV, D, torch.bfloat16, dev)
+    table_d = w["table"].to(dev)
+    lens_d = w["lengths"].to(dev)
+    meta = AttentionMetadata(BatchPhase.DECODE, block_table=table_d, cache_seqlens=lens_d)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    plan = prepare_decode_plan(None, meta, spec, 1, graph=False)
+    torch.cuda.synchronize()
+    plan_ms = (time.perf_counter() - t0) * 1e3
+    info = plan.info()
+    out = torch.empty_like(w["q"])
+
+    def step():
+        cache.write_kv(w["knew"], w["vnew"], w["loc"])
+        run_decode(plan, w["q"], w["kc"], w["vc"], out)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # Decode kernels alone, HIP events on the current (launch) stream.
+    reps = max(args.steps, 20)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run_decode(plan, w["q"], w["kc"], w["vc"], out)
+    e1.record()
+    torch.cuda.synchronize()
+    decode_ms = e0.elapsed_time(e1) / reps
+    e0.record()
+    for _ in range(reps):
+        cache.write_kv(w["knew"], w["vnew"], w["loc"])
+    e1.record()
+    torch.cuda.synchronize()
+    store_ms = e0.elapsed_time(e1) / reps
+    cache.check_write_errors()
+
+    dbytes = decode_bytes(w["lengths"], HQ, HKV, D)
+    sbytes = store_bytes(B, HKV, D)
+    achieved = dbytes / (decode_ms * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round((dbytes + sbytes) / (step_ms * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, seeded randperm page table)",
+        "config": {"workload": "cfg2 paged decode + KV store: B=64, Hq16/Hkv8, D128, "
+                               "L~U[512,4096], page 1, 4M-slot pool",
+                   "kv_tokens": int(w["lengths"].sum()), "page_size": 1,
+                   "split_kv_items": info["num_items"], "chunk_tokens": info["chunk_tokens"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "decode_kernel+merge_kernel (one mi355x_decode_run)",
+                     "algorithmic_bytes": dbytes, "avg_launch_us": round(decode_ms * 1e3, 3)},
+        "kv_store": {"us": round(store_ms * 1e3, 3), "bytes": sbytes,
+                     "GB/s": round(sbytes / (store_ms * 1e-3) / 1e9, 2)},
+        "plan_prepare_ms": round(plan_ms, 3),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w, args.cpu_requests)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

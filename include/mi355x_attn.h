@@ -1,0 +1,149 @@
+/*
+ * mi355x_attn.h - C ABI of the gfx950 attention hot path (libmi355x_attn.so).
+ *
+ * Drop-in boundary for the reference server's native attention, KV-store and
+ * norm bridges (MabinogiX/llm_infer_rust). Every function takes raw device
+ * pointers, element strides, a dtype code (0 = bfloat16, 1 = float16) and a
+ * hipStream_t passed as void*. No ATen/torch types cross this boundary.
+ *
+ * Error convention (same as the reference's raw sglang_native_* launchers):
+ * functions returning `const char*` return NULL on success and otherwise a
+ * message that stays valid until the next failing call on the same thread.
+ * Plan-returning functions return NULL on failure; mi355x_attn_error() then
+ * holds the message (the reference's thread-local last_error,
+ * src/models/attention/flashinfer_bridge.cpp:13,59).
+ *
+ * Threading: a plan is owned by one host thread (the reference's plans are
+ * Rc, not Send). All work is enqueued on the given stream; nothing blocks
+ * except where stated.
+ */
+#ifndef MI355X_ATTN_H
+#define MI355X_ATTN_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#pragma GCC visibility push(default)
+
+/* Last error of a plan-returning call on this thread.
+ * Replaces sglang_flashinfer_error / sglang_layers_error / sglang_store_kv_error
+ * (flashinfer_bridge.cpp:59, fused_ops_bridge.cpp:56, kv_store_bridge.cpp:11). */
+const char* mi355x_attn_error(void);
+
+/* ABI revision of this header (currently 1). No reference counterpart. */
+int mi355x_attn_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * K/V store. kc[loc[t]] = k[t], vc[loc[t]] = v[t] bitwise for 16-bit
+ * elements. k/v are [tokens, heads, width] with strides (kt, kh, 1); caches
+ * are contiguous [capacity, heads, width]. loc is int32 or int64 (index64).
+ * A slot equal to `reserved` is skipped. A slot outside [0, capacity) is not
+ * written; if `error_count` (device int32) is non-NULL it is incremented once
+ * per such token, so the caller can raise the error the reference raises.
+ * Replaces sglang_native_store_kv (src/models/attention/kv_store.cu:65-68).
+ * ------------------------------------------------------------------------ */
+const char* mi355x_store_kv(const void* k, const void* v, void* kc, void* vc, const void* loc,
+                            int64_t tokens, int64_t heads, int64_t width, int64_t capacity,
+                            int64_t kt, int64_t kh, int64_t vt, int64_t vh, int64_t reserved,
+                            bool index64, int32_t* error_count, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Norms (fp32 accumulation, output rounded to the activation dtype).
+ * ------------------------------------------------------------------------ */
+
+/* out[(t*heads+h), :] = x[t,h,:] * rsqrt(mean(x^2) + eps) * weight; out contiguous.
+ * Replaces sglang_layers_native_norm (src/layers/fused_ops.cu:210-213). */
+const char* mi355x_rms_norm(const void* x, const void* weight, void* out, int64_t tokens,
+                            int64_t heads, int64_t width, int64_t token_stride,
+                            int64_t head_stride, double eps, int dtype, void* stream);
+
+/* In place: s = x + residual (fp32); residual <- round(s); x <- round(rms(s) * w).
+ * x and residual must not alias.
+ * Replaces sglang_layers_native_add_norm (src/layers/fused_ops.cu:300-303). */
+const char* mi355x_add_rms_norm(void* x, void* residual, const void* weight, int64_t tokens,
+                                int64_t width, int64_t x_stride, int64_t residual_stride,
+                                double eps, int dtype, void* stream);
+
+/* In place per-head RMSNorm of q [tokens, q_heads, width] with q_weight and of
+ * k [tokens, k_heads, width] with k_weight. Nothing else is written.
+ * Replaces sglang_layers_native_qk_norm (src/layers/fused_ops.cu:254-259). */
+const char* mi355x_qk_norm(void* q, void* k, const void* q_weight, const void* k_weight,
+                           int64_t tokens, int64_t q_heads, int64_t k_heads, int64_t width,
+                           int64_t q_token_stride, int64_t q_head_stride,
+                           int64_t k_token_stride, int64_t k_head_stride, double eps, int dtype,
+                           void* stream);
+
+/* ------------------------------------------------------------------------
+ * Paged decode attention (head_dim 128, q heads per kv head in {1,2,4,8}).
+ * ------------------------------------------------------------------------ */
+
+/* Build or refresh a decode plan once per forward; every layer reuses it.
+ * block_table: device int32 [batch, columns] with row stride table_stride;
+ * seq_lens: device int32 [batch]. host_lengths (nullable, host_rows entries)
+ * is the scheduler's host copy of seq_lens; without it the lengths are read
+ * back once (blocking). The plan packs the reference page metadata
+ * (indptr / indices / last_page_len) and a split-KV work list sized for the
+ * device's CU count. `existing` must have the same geometry; with graph=true
+ * the rows/columns are fixed and workspaces never move.
+ * Replaces sglang_flashinfer_prepare (flashinfer_bridge.cpp:61-65). */
+void* mi355x_decode_prepare(void* existing, const int32_t* block_table, int64_t batch,
+                            int64_t columns, int64_t table_stride, const int32_t* seq_lens,
+                            int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                            int64_t page_size, int64_t dtype, bool graph,
+                            const int32_t* host_lengths, int64_t host_rows, void* stream);
+
+/* out[b, h, :] = softmax(q[b,h] K^T / sqrt(128)) V over the request's pages.
+ * q/out: [batch, num_q_heads, 128] with the given strides (16-byte aligned
+ * rows); caches: contiguous [pages, page_size, num_kv_heads, 128].
+ * Replaces sglang_flashinfer_decode (flashinfer_bridge.cpp:201-203) and
+ * sglang_flashinfer_native_run (flashinfer_plan_run.cu:222-227). */
+const char* mi355x_decode_run(const void* plan, const void* q, int64_t q_stride_n,
+                              int64_t q_stride_h, const void* k_cache, const void* v_cache,
+                              void* out, int64_t out_stride_n, int64_t out_stride_h,
+                              int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                              int64_t page_size, int64_t dtype, void* stream);
+
+/* Frees a plan after waiting for its pending uploads.
+ * Replaces sglang_flashinfer_plan_drop (flashinfer_bridge.cpp:192-199). */
+void mi355x_decode_plan_drop(void* plan);
+
+/* Number of workspace (re)allocations made by the plan so far.
+ * Replaces sglang_flashinfer_workspace_allocations (flashinfer_bridge.cpp:187-190). */
+uint64_t mi355x_decode_workspace_allocations(const void* plan);
+
+/* Plan facts: out6 = {batch, total_pages, num_items, chunk_tokens,
+ * items_capacity, cus}. Introspection; no reference counterpart. */
+const char* mi355x_decode_plan_info(const void* plan, int64_t* out6);
+
+/* Blocking copy of the plan's page metadata and work list to host memory
+ * (indptr batch+1, indices total_pages, last_len batch, work 4*num_items,
+ * merge 2*batch ints; any pointer may be NULL). Introspection for parity
+ * tests; no reference counterpart. */
+const char* mi355x_decode_plan_read(const void* plan, int32_t* indptr, int32_t* indices,
+                                    int32_t* last_len, int32_t* work, int32_t* merge,
+                                    void* stream);
+
+/* Host-only split-KV scheduler used by mi355x_decode_prepare: fills `work`
+ * (4 ints per item: request, token_begin, token_end, partial slot or -1) and
+ * `merge` (2 ints per request: first partial slot or -1, chunk count).
+ * Returns the item count, or -1 on invalid input / insufficient capacity.
+ * Stands in for FlashInfer's DecodePlan work estimation
+ * (flashinfer_plan_run.cu:74-112). */
+int64_t mi355x_decode_schedule(const int32_t* lengths, int64_t batch, int64_t cus,
+                               int64_t num_kv_heads, int32_t* work, int64_t work_capacity,
+                               int32_t* merge, int64_t* chunk_tokens);
+
+/* Work-list capacity a plan reserves for `rows` requests. */
+int64_t mi355x_decode_items_capacity(int64_t rows, int64_t cus, int64_t num_kv_heads);
+
+#pragma GCC visibility pop
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355X_ATTN_H */

@@ -1,0 +1,137 @@
+// Shared device/host helpers for the gfx950 attention hot path.
+//
+// Element types are carried as raw 16-bit words (uint16_t). dtype code 0 is
+// bfloat16 and 1 is float16, the same codes the reference server passes
+// through its native ABI (src/models/attention/flashinfer_bridge.cpp:81,
+// src/layers/fused_ops.cu:210-213).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "mi355x_attn.h"
+
+namespace mi355x {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+// ----------------------------------------------------------------------------
+// Error plumbing: every raw entry point returns NULL on success, otherwise a
+// pointer to a thread-local message that stays valid until the next failing
+// call on the same thread.
+// ----------------------------------------------------------------------------
+const char* set_error(const std::string& message);
+const char* hip_error(hipError_t status, const char* what);
+const char* launch_status(const char* what);
+
+inline bool aligned(const void* p, uintptr_t a) {
+  return reinterpret_cast<uintptr_t>(p) % a == 0;
+}
+
+// ----------------------------------------------------------------------------
+// 16-bit float conversions. bf16 -> f32 is exact (shift); f32 -> bf16 rounds
+// to nearest-even with NaN kept quiet, which is what torch's CPU and GPU
+// casts do, so residual write-backs compare bit-exactly.
+// ----------------------------------------------------------------------------
+template <int DT>
+struct Elem;
+
+template <>
+struct Elem<0> {  // bfloat16
+  __device__ __forceinline__ static float to_float(uint16_t h) {
+    return __uint_as_float(static_cast<uint32_t>(h) << 16);
+  }
+  __device__ __forceinline__ static uint16_t from_float(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+  }
+};
+
+template <>
+struct Elem<1> {  // float16
+  __device__ __forceinline__ static float to_float(uint16_t h) {
+    _Float16 v = __builtin_bit_cast(_Float16, h);
+    return static_cast<float>(v);
+  }
+  __device__ __forceinline__ static uint16_t from_float(float f) {
+    _Float16 v = static_cast<_Float16>(f);  // round-to-nearest-even
+    return __builtin_bit_cast(uint16_t, v);
+  }
+};
+
+// Unpack 8 packed 16-bit values (one 128-bit load) into floats.
+template <int DT>
+__device__ __forceinline__ void unpack8(const uint4& w, float (&f)[8]) {
+  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = Elem<DT>::to_float(static_cast<uint16_t>(words[i] & 0xffffu));
+    f[2 * i + 1] = Elem<DT>::to_float(static_cast<uint16_t>(words[i] >> 16));
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
+  uint32_t words[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    words[i] = static_cast<uint32_t>(Elem<DT>::from_float(f[2 * i])) |
+               (static_cast<uint32_t>(Elem<DT>::from_float(f[2 * i + 1])) << 16);
+  }
+  return make_uint4(words[0], words[1], words[2], words[3]);
+}
+
+// ----------------------------------------------------------------------------
+// Cross-lane reductions built on DPP row operations. A DPP "row" is 16 lanes,
+// so a 16-lane sum needs four register-to-register steps and no LDS traffic:
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
+// Every lane of the row ends up holding the row total.
+// ----------------------------------------------------------------------------
+constexpr int kDppQuadSwap1 = 0xB1;      // quad_perm(1,0,3,2)
+constexpr int kDppQuadSwap2 = 0x4E;      // quad_perm(2,3,0,1)
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), Ctrl, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp<kDppQuadSwap1>(x);
+  x += dpp<kDppQuadSwap2>(x);
+  x += dpp<kDppRowHalfMirror>(x);
+  x += dpp<kDppRowMirror>(x);
+  return x;
+}
+
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp<kDppQuadSwap1>(x));
+  x = fmaxf(x, dpp<kDppQuadSwap2>(x));
+  x = fmaxf(x, dpp<kDppRowHalfMirror>(x));
+  x = fmaxf(x, dpp<kDppRowMirror>(x));
+  return x;
+}
+
+// Sum over the whole 64-lane wave; all lanes receive the total.
+__device__ __forceinline__ float wave_sum(float x) {
+  x = row16_sum(x);
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+// 128-bit global loads/stores.
+__device__ __forceinline__ uint4 ld128(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+__device__ __forceinline__ void st128(void* p, const uint4& v) {
+  *reinterpret_cast<uint4*>(p) = v;
+}
+
+}  // namespace mi355x

@@ -1,0 +1,702 @@
+// Paged decode attention for gfx950: per-forward plan (page metadata + split-KV
+// work list) and the decode / merge kernels.
+//
+// Reference path this replaces:
+//   plan:  sglang_flashinfer_prepare   src/models/attention/flashinfer_bridge.cpp:61-185
+//          pack_decode_metadata        src/models/attention/flashinfer_plan_run.cu:24-34
+//          DecodePlan (work estimation) flashinfer_plan_run.cu:74-125
+//   run:   sglang_flashinfer_decode    flashinfer_bridge.cpp:201-240
+//          BatchDecodeWithPagedKVCacheDispatched  flashinfer_plan_run.cu:127-173
+//   math:  o[b,h] = softmax_j(q[b,h] . k[j,h/g] * sm_scale) v[j,h/g], j over the
+//          request's cache_seqlens[b] tokens, sm_scale = 1/sqrt(128)
+//          (backend.rs:1375-1420 decode_with_cache_padded is the libtorch restatement).
+//
+// Page metadata is the reference's closed form, bit for bit:
+//   indptr[0] = 0, indptr[r+1] = indptr[r] + ceil(len[r] / P)
+//   indices[indptr[r] + c] = block_table[r * stride + c], c < ceil(len[r] / P)
+//   last_page_len[r] = (len[r] - 1) % P + 1
+//
+// Split-KV schedule (our own design for 256 CUs): every request's tokens are cut
+// into chunks of `chunk_tokens` (a multiple of 16) chosen so that the number of
+// (request, chunk) work items is about 4 per CU. One workgroup handles one work
+// item for up to 8 KV heads (one wave per KV head), so the 2 KiB K row and the
+// 2 KiB V row of a page-size-1 slot are fetched by one workgroup at the same
+// time. A request that fits one chunk writes its output directly; others
+// write normalised fp32 partials + log2-sum-exp, combined by the merge kernel.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <memory>
+#include <vector>
+
+#include "common.h"
+
+namespace mi355x {
+namespace {
+
+constexpr int kHeadDim = 128;
+constexpr int kTokensPerLaneGroup = 4;  // tokens per 16-lane group per loop trip
+constexpr int kTileTokens = 4 * kTokensPerLaneGroup;
+constexpr int kMaxWavesPerBlock = 8;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------------------
+// Device buffer with geometric growth, matching the reference workspace rule
+// (flashinfer_plan_run.cu:47-65): grow x2 from 64 KiB, count allocations.
+// ---------------------------------------------------------------------------
+struct DeviceBuffer {
+  void* ptr = nullptr;
+  size_t capacity = 0;
+  bool pinned = false;
+
+  hipError_t reserve(size_t bytes, uint64_t& allocations) {
+    if (bytes <= capacity) return hipSuccess;
+    size_t grown = std::max(bytes, capacity ? capacity * 2 : size_t(65536));
+    void* fresh = nullptr;
+    hipError_t st = pinned ? hipHostMalloc(&fresh, grown, hipHostMallocDefault)
+                           : hipMalloc(&fresh, grown);
+    if (st != hipSuccess) return st;
+    if (!pinned) {
+      st = hipMemset(fresh, 0, grown);
+      if (st != hipSuccess) {
+        (void)hipFree(fresh);
+        return st;
+      }
+    }
+    release();
+    ptr = fresh;
+    capacity = grown;
+    ++allocations;
+    return hipSuccess;
+  }
+  void release() {
+    if (ptr) {
+      if (pinned)
+        (void)hipHostFree(ptr);
+      else
+        (void)hipFree(ptr);
+    }
+    ptr = nullptr;
+    capacity = 0;
+  }
+  ~DeviceBuffer() { release(); }
+};
+
+// int32 workspace layout (device and pinned staging share it):
+//   [0]                  number of work items
+//   [4, 4+B+1)           indptr
+//   [o_work, +4*cap)     work items {request, token_begin, token_end, partial}
+//   [o_merge, +2*B)      per-request {first partial, chunk count}
+struct IntLayout {
+  int64_t o_indptr, o_work, o_merge, total;
+  static IntLayout make(int64_t rows, int64_t items_cap) {
+    IntLayout l{};
+    l.o_indptr = 4;
+    l.o_work = (l.o_indptr + rows + 1 + 3) / 4 * 4;
+    l.o_merge = l.o_work + 4 * items_cap;
+    l.total = l.o_merge + 2 * rows;
+    return l;
+  }
+};
+
+}  // namespace
+
+struct DecodePlan {
+  int device = -1;
+  int64_t num_q_heads = 0, num_kv_heads = 0, head_dim = 0, page_size = 0, dtype = 0;
+  bool graph = false;
+  int64_t graph_rows = 0, graph_columns = 0;
+  // Current plan facts.
+  int64_t batch = 0, total_pages = 0, num_items = 0, chunk_tokens = 0, items_capacity = 0;
+  int64_t cus = 0;
+  IntLayout layout{};
+  DeviceBuffer ints, indices, last_len, partial_o, partial_lse;
+  DeviceBuffer staging;
+  hipEvent_t upload_done = nullptr;
+  uint64_t allocations = 0;
+  std::vector<int32_t> host_lengths;
+
+  DecodePlan() { staging.pinned = true; }
+  ~DecodePlan() {
+    if (upload_done) {
+      (void)hipEventSynchronize(upload_done);
+      (void)hipEventDestroy(upload_done);
+    }
+  }
+};
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Host planner: split-KV work list. Pure host code.
+// ---------------------------------------------------------------------------
+int64_t target_items_for(int64_t cus, int64_t num_kv_heads) {
+  const int64_t waves = std::min<int64_t>(num_kv_heads, kMaxWavesPerBlock);
+  const int64_t grid_y = (num_kv_heads + waves - 1) / waves;
+  // About 32 resident waves per CU; keep ~1 full round of workgroups.
+  const int64_t per_cu = std::max<int64_t>(1, 32 / waves);
+  return std::max<int64_t>(1, cus * per_cu / grid_y);
+}
+
+int64_t items_capacity_for(int64_t rows, int64_t cus, int64_t num_kv_heads) {
+  return rows + target_items_for(cus, num_kv_heads);
+}
+
+// Fills work (4 ints per item) and merge (2 ints per request). Returns the item
+// count, or -1 when `capacity` is too small.
+int64_t schedule(const int32_t* lengths, int64_t batch, int64_t cus, int64_t num_kv_heads,
+                 int32_t* work, int64_t capacity, int32_t* merge, int64_t* chunk_out) {
+  int64_t total = 0, longest = 0;
+  for (int64_t r = 0; r < batch; ++r) {
+    total += lengths[r];
+    longest = std::max<int64_t>(longest, lengths[r]);
+  }
+  const int64_t target = target_items_for(cus, num_kv_heads);
+  int64_t chunk;
+  if (batch >= target) {
+    chunk = longest;  // enough requests to fill the chip without splitting
+  } else {
+    const int64_t min_chunk = 128;
+    chunk = std::max<int64_t>((total + target - 1) / target, min_chunk);
+    chunk = (chunk + kTileTokens - 1) / kTileTokens * kTileTokens;
+    if (chunk >= longest) chunk = longest;
+  }
+  chunk = std::max<int64_t>(chunk, 1);
+  int64_t items = 0, partials = 0;
+  for (int64_t r = 0; r < batch; ++r) {
+    const int64_t len = lengths[r];
+    const int64_t n = (len + chunk - 1) / chunk;
+    merge[2 * r] = static_cast<int32_t>(n > 1 ? partials : -1);
+    merge[2 * r + 1] = static_cast<int32_t>(n);
+    for (int64_t c = 0; c < n; ++c) {
+      if (items >= capacity) return -1;
+      work[4 * items + 0] = static_cast<int32_t>(r);
+      work[4 * items + 1] = static_cast<int32_t>(c * chunk);
+      work[4 * items + 2] = static_cast<int32_t>(std::min(len, (c + 1) * chunk));
+      work[4 * items + 3] = static_cast<int32_t>(n > 1 ? partials + c : -1);
+      ++items;
+    }
+    if (n > 1) partials += n;
+  }
+  *chunk_out = chunk;
+  return items;
+}
+
+// ---------------------------------------------------------------------------
+// Page metadata pack: one workgroup per request.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pack_page_metadata(const int32_t* __restrict__ table,
+                                                          const int32_t* __restrict__ lengths,
+                                                          const int32_t* __restrict__ indptr,
+                                                          int32_t* __restrict__ indices,
+                                                          int32_t* __restrict__ last_len,
+                                                          int64_t stride, int32_t page_size) {
+  const int row = blockIdx.x;
+  const int begin = indptr[row];
+  const int pages = indptr[row + 1] - begin;
+  if (threadIdx.x == 0) last_len[row] = (lengths[row] - 1) % page_size + 1;
+  const int32_t* src = table + row * stride;
+  for (int c = threadIdx.x; c < pages; c += blockDim.x) indices[begin + c] = src[c];
+}
+
+// ---------------------------------------------------------------------------
+// Decode kernel.
+// ---------------------------------------------------------------------------
+struct DecodeArgs {
+  const uint16_t* q;
+  int64_t q_stride_n, q_stride_h;
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  uint16_t* out;
+  int64_t out_stride_n, out_stride_h;
+  const int32_t* ints;  // workspace (num_items, indptr, work, merge)
+  int32_t o_indptr, o_work, o_merge;
+  const int32_t* indices;
+  float* partial_o;
+  float* partial_lse;
+  int32_t num_q_heads, num_kv_heads, page_size;
+  float scale_log2;  // sm_scale * log2(e)
+};
+
+// 8-element dot product of packed 16-bit vectors with fp32 accumulation
+// (v_dot2c_f32_bf16 / v_dot2c_f32_f16).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+template <int DT>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (DT == 0) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+  } else {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b),
+                                  c, false);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float dot8(const uint4& a, const uint4& b) {
+  float s = dot2<DT>(a.x, b.x, 0.f);
+  s = dot2<DT>(a.y, b.y, s);
+  s = dot2<DT>(a.z, b.z, s);
+  s = dot2<DT>(a.w, b.w, s);
+  return s;
+}
+
+template <int DT, int G, bool P1>
+__global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.y * (blockDim.x >> 6) + wave;  // kv head
+  const int item = blockIdx.x;
+  if (h >= a.num_kv_heads || item >= a.ints[0]) return;  // uniform per wave
+
+  const int4 w = reinterpret_cast<const int4*>(a.ints + a.o_work)[item];
+  const int req = w.x, beg = w.y, end = w.z, pslot = w.w;
+  const int grp = lane >> 4, sub = lane & 15;
+
+  // Query rows of the G heads that share kv head h, kept packed (8 x 16-bit).
+  uint4 qv[G];
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi)
+    qv[gi] = ld128(a.q + req * a.q_stride_n + (h * G + gi) * a.q_stride_h + sub * 8);
+
+  const int32_t* pages = a.indices + a.ints[a.o_indptr + req];
+  const int64_t row_elems = static_cast<int64_t>(a.num_kv_heads) * kHeadDim;
+  const uint16_t* kbase = a.k_cache + h * kHeadDim + sub * 8;
+  const uint16_t* vbase = a.v_cache + h * kHeadDim + sub * 8;
+
+  float m[G], l[G], o[G][8];
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    m[gi] = -1e30f;
+    l[gi] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[gi][i] = 0.f;
+  }
+
+  for (int t0 = beg; t0 < end; t0 += kTileTokens) {
+    uint4 kr[kTokensPerLaneGroup], vr[kTokensPerLaneGroup];
+    bool valid[kTokensPerLaneGroup];
+#pragma unroll
+    for (int u = 0; u < kTokensPerLaneGroup; ++u) {
+      const int t = t0 + u * 4 + grp;
+      valid[u] = t < end;
+      const int tt = valid[u] ? t : beg;
+      int64_t slot;
+      if constexpr (P1) {
+        slot = pages[tt];
+      } else {
+        slot = static_cast<int64_t>(pages[tt / a.page_size]) * a.page_size + tt % a.page_size;
+      }
+      kr[u] = ld128(kbase + slot * row_elems);
+      vr[u] = ld128(vbase + slot * row_elems);
+    }
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      float s[kTokensPerLaneGroup];
+      float mx = m[gi];
+#pragma unroll
+      for (int u = 0; u < kTokensPerLaneGroup; ++u) {
+        s[u] = row16_sum(dot8<DT>(qv[gi], kr[u])) * a.scale_log2;
+        s[u] = valid[u] ? s[u] : -INFINITY;
+        mx = fmaxf(mx, s[u]);
+      }
+      const float corr = __builtin_amdgcn_exp2f(m[gi] - mx);
+      m[gi] = mx;
+      l[gi] *= corr;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[gi][i] *= corr;
+#pragma unroll
+      for (int u = 0; u < kTokensPerLaneGroup; ++u) {
+        const float p = __builtin_amdgcn_exp2f(s[u] - mx);
+        l[gi] += p;
+        float vf[8];
+        unpack8<DT>(vr[u], vf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[gi][i] = fmaf(p, vf[i], o[gi][i]);
+      }
+    }
+  }
+
+  // Combine the four 16-lane groups of the wave (each saw a token subset).
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    float mx = fmaxf(m[gi], __shfl_xor(m[gi], 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float f = __builtin_amdgcn_exp2f(m[gi] - mx);
+    float lv = l[gi] * f;
+    lv += __shfl_xor(lv, 16);
+    lv += __shfl_xor(lv, 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float x = o[gi][i] * f;
+      x += __shfl_xor(x, 16);
+      x += __shfl_xor(x, 32);
+      o[gi][i] = x / lv;
+    }
+    m[gi] = mx;
+    l[gi] = lv;
+  }
+  if (grp != 0) return;
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    const int qh = h * G + gi;
+    if (pslot < 0) {
+      st128(a.out + req * a.out_stride_n + qh * a.out_stride_h + sub * 8, pack8<DT>(o[gi]));
+    } else {
+      float* dst = a.partial_o + (static_cast<int64_t>(pslot) * a.num_q_heads + qh) * kHeadDim +
+                   sub * 8;
+      *reinterpret_cast<float4*>(dst) = make_float4(o[gi][0], o[gi][1], o[gi][2], o[gi][3]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[gi][4], o[gi][5], o[gi][6], o[gi][7]);
+      if (sub == 0)
+        a.partial_lse[static_cast<int64_t>(pslot) * a.num_q_heads + qh] =
+            m[gi] + __builtin_amdgcn_logf(l[gi]);
+    }
+  }
+}
+
+// Merge split-KV partials: one wave per (request, q head), two dims per lane.
+template <int DT>
+__global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a, int32_t rows) {
+  const int req = blockIdx.x;
+  const int qh = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (req >= rows || qh >= a.num_q_heads) return;
+  const int first = a.ints[a.o_merge + 2 * req];
+  const int count = a.ints[a.o_merge + 2 * req + 1];
+  if (count <= 1) return;
+  float mx = -INFINITY;
+  for (int c = 0; c < count; ++c)
+    mx = fmaxf(mx, a.partial_lse[static_cast<int64_t>(first + c) * a.num_q_heads + qh]);
+  float acc0 = 0.f, acc1 = 0.f, den = 0.f;
+  for (int c = 0; c < count; ++c) {
+    const int64_t p = static_cast<int64_t>(first + c) * a.num_q_heads + qh;
+    const float wgt = __builtin_amdgcn_exp2f(a.partial_lse[p] - mx);
+    const float2 v = *reinterpret_cast<const float2*>(a.partial_o + p * kHeadDim + lane * 2);
+    acc0 = fmaf(wgt, v.x, acc0);
+    acc1 = fmaf(wgt, v.y, acc1);
+    den += wgt;
+  }
+  const uint32_t packed =
+      static_cast<uint32_t>(Elem<DT>::from_float(acc0 / den)) |
+      (static_cast<uint32_t>(Elem<DT>::from_float(acc1 / den)) << 16);
+  *reinterpret_cast<uint32_t*>(a.out + req * a.out_stride_n + qh * a.out_stride_h + lane * 2) =
+      packed;
+}
+
+template <int DT, int G>
+void launch_decode(const DecodeArgs& a, dim3 grid, int waves, bool p1, hipStream_t s) {
+  const dim3 block(waves * kWave);
+  if (p1)
+    decode_kernel<DT, G, true><<<grid, block, 0, s>>>(a);
+  else
+    decode_kernel<DT, G, false><<<grid, block, 0, s>>>(a);
+}
+
+template <int DT>
+bool dispatch_group(const DecodeArgs& a, int group, dim3 grid, int waves, bool p1,
+                    hipStream_t s) {
+  switch (group) {
+    case 1: launch_decode<DT, 1>(a, grid, waves, p1, s); return true;
+    case 2: launch_decode<DT, 2>(a, grid, waves, p1, s); return true;
+    case 4: launch_decode<DT, 4>(a, grid, waves, p1, s); return true;
+    case 8: launch_decode<DT, 8>(a, grid, waves, p1, s); return true;
+    default: return false;
+  }
+}
+
+}  // namespace
+}  // namespace mi355x
+
+using namespace mi355x;
+
+extern "C" int64_t mi355x_decode_schedule(const int32_t* lengths, int64_t batch, int64_t cus,
+                                          int64_t num_kv_heads, int32_t* work,
+                                          int64_t work_capacity, int32_t* merge,
+                                          int64_t* chunk_tokens) {
+  if (!lengths || batch < 0 || cus <= 0 || num_kv_heads <= 0 || !work || !merge || !chunk_tokens)
+    return -1;
+  for (int64_t r = 0; r < batch; ++r)
+    if (lengths[r] <= 0) return -1;
+  return schedule(lengths, batch, cus, num_kv_heads, work, work_capacity, merge, chunk_tokens);
+}
+
+extern "C" int64_t mi355x_decode_items_capacity(int64_t rows, int64_t cus, int64_t num_kv_heads) {
+  if (rows < 0 || cus <= 0 || num_kv_heads <= 0) return -1;
+  return items_capacity_for(rows, cus, num_kv_heads);
+}
+
+extern "C" void* mi355x_decode_prepare(void* existing, const int32_t* block_table,
+                                       int64_t batch, int64_t columns, int64_t table_stride,
+                                       const int32_t* seq_lens, int64_t num_q_heads,
+                                       int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                                       int64_t dtype, bool graph, const int32_t* host_lengths,
+                                       int64_t host_rows, void* stream) {
+  auto s = static_cast<hipStream_t>(stream);
+  std::unique_ptr<DecodePlan> created;
+  DecodePlan* plan = static_cast<DecodePlan*>(existing);
+  try {
+    if (!block_table || !seq_lens || batch <= 0 || columns <= 0 || table_stride < columns) {
+      set_error("invalid decode block table or lengths");
+      return nullptr;
+    }
+    if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
+        head_dim != kHeadDim || page_size <= 0 || (dtype != 0 && dtype != 1)) {
+      set_error("unsupported decode attention configuration");
+      return nullptr;
+    }
+    const int64_t group = num_q_heads / num_kv_heads;
+    if (group != 1 && group != 2 && group != 4 && group != 8) {
+      set_error("decode attention supports 1, 2, 4 or 8 query heads per kv head");
+      return nullptr;
+    }
+    int device = 0;
+    hipError_t st = hipGetDevice(&device);
+    if (st != hipSuccess) {
+      hip_error(st, "hipGetDevice");
+      return nullptr;
+    }
+    if (plan && (plan->device != device || plan->num_q_heads != num_q_heads ||
+                 plan->num_kv_heads != num_kv_heads || plan->head_dim != head_dim ||
+                 plan->page_size != page_size || plan->dtype != dtype || plan->graph != graph ||
+                 (graph && (plan->graph_columns != columns || plan->graph_rows != batch)))) {
+      set_error("decode workspace geometry changed");
+      return nullptr;
+    }
+    if (!plan) {
+      created = std::make_unique<DecodePlan>();
+      plan = created.get();
+      plan->device = device;
+      int cus = 0;
+      st = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+      if (st != hipSuccess) {
+        hip_error(st, "hipDeviceGetAttribute");
+        return nullptr;
+      }
+      plan->cus = std::max(cus, 1);
+      plan->num_q_heads = num_q_heads;
+      plan->num_kv_heads = num_kv_heads;
+      plan->head_dim = head_dim;
+      plan->page_size = page_size;
+      plan->dtype = dtype;
+      plan->graph = graph;
+      plan->graph_rows = batch;
+      plan->graph_columns = columns;
+      st = hipEventCreateWithFlags(&plan->upload_done, hipEventDisableTiming);
+      if (st != hipSuccess) {
+        hip_error(st, "hipEventCreate");
+        return nullptr;
+      }
+    }
+
+    // Host lengths: the scheduler's snapshot when given, else one D2H read.
+    plan->host_lengths.resize(batch);
+    if (host_lengths) {
+      if (host_rows != batch) {
+        set_error("invalid host decode metadata");
+        return nullptr;
+      }
+      std::memcpy(plan->host_lengths.data(), host_lengths, batch * sizeof(int32_t));
+    } else {
+      st = hipMemcpyAsync(plan->host_lengths.data(), seq_lens, batch * sizeof(int32_t),
+                          hipMemcpyDeviceToHost, s);
+      if (st == hipSuccess) st = hipStreamSynchronize(s);
+      if (st != hipSuccess) {
+        hip_error(st, "decode length readback");
+        return nullptr;
+      }
+    }
+    int64_t total_pages = 0;
+    for (int64_t r = 0; r < batch; ++r) {
+      const int64_t len = plan->host_lengths[r];
+      if (len <= 0 || len > columns * page_size) {
+        set_error("host cache length exceeds block table capacity");
+        return nullptr;
+      }
+      total_pages += (len + page_size - 1) / page_size;
+      if (total_pages > std::numeric_limits<int32_t>::max()) {
+        set_error("page indptr overflow");
+        return nullptr;
+      }
+    }
+
+    const int64_t items_cap = items_capacity_for(batch, plan->cus, num_kv_heads);
+    const IntLayout layout = IntLayout::make(batch, items_cap);
+    const size_t int_bytes = layout.total * sizeof(int32_t);
+    const size_t idx_bytes = static_cast<size_t>(batch) * columns * sizeof(int32_t);
+    const size_t part_o_bytes = static_cast<size_t>(items_cap) * num_q_heads * kHeadDim * 4;
+    const size_t part_lse_bytes = static_cast<size_t>(items_cap) * num_q_heads * 4;
+    const size_t last_bytes = static_cast<size_t>(batch) * sizeof(int32_t);
+    if (graph && !created &&
+        (int_bytes > plan->ints.capacity || idx_bytes > plan->indices.capacity ||
+         part_o_bytes > plan->partial_o.capacity || last_bytes > plan->last_len.capacity)) {
+      set_error("graph decode metadata capacity exceeded");
+      return nullptr;
+    }
+    // The pinned staging buffer may still be feeding the previous upload.
+    st = hipEventSynchronize(plan->upload_done);
+    if (st != hipSuccess) {
+      hip_error(st, "decode upload fence");
+      return nullptr;
+    }
+    if ((st = plan->ints.reserve(int_bytes, plan->allocations)) != hipSuccess ||
+        (st = plan->indices.reserve(idx_bytes, plan->allocations)) != hipSuccess ||
+        (st = plan->last_len.reserve(last_bytes, plan->allocations)) != hipSuccess ||
+        (st = plan->partial_o.reserve(part_o_bytes, plan->allocations)) != hipSuccess ||
+        (st = plan->partial_lse.reserve(part_lse_bytes, plan->allocations)) != hipSuccess ||
+        (st = plan->staging.reserve(int_bytes, plan->allocations)) != hipSuccess) {
+      hip_error(st, "decode workspace allocation");
+      return nullptr;
+    }
+    int32_t* host = static_cast<int32_t*>(plan->staging.ptr);
+    std::memset(host, 0, int_bytes);
+    int32_t* indptr = host + layout.o_indptr;
+    indptr[0] = 0;
+    for (int64_t r = 0; r < batch; ++r)
+      indptr[r + 1] = indptr[r] + static_cast<int32_t>(
+                                      (plan->host_lengths[r] + page_size - 1) / page_size);
+    int64_t chunk = 0;
+    const int64_t items = schedule(plan->host_lengths.data(), batch, plan->cus, num_kv_heads,
+                                   host + layout.o_work, items_cap, host + layout.o_merge, &chunk);
+    if (items < 0) {
+      set_error("decode work list exceeds its capacity");
+      return nullptr;
+    }
+    host[0] = static_cast<int32_t>(items);
+    st = hipMemcpyAsync(plan->ints.ptr, host, int_bytes, hipMemcpyHostToDevice, s);
+    if (st != hipSuccess) {
+      hip_error(st, "decode metadata upload");
+      return nullptr;
+    }
+    pack_page_metadata<<<dim3(static_cast<uint32_t>(batch)), dim3(256), 0, s>>>(
+        block_table, seq_lens, static_cast<const int32_t*>(plan->ints.ptr) + layout.o_indptr,
+        static_cast<int32_t*>(plan->indices.ptr), static_cast<int32_t*>(plan->last_len.ptr),
+        table_stride, static_cast<int32_t>(page_size));
+    if (const char* err = launch_status("pack_page_metadata")) {
+      (void)err;
+      return nullptr;
+    }
+    st = hipEventRecord(plan->upload_done, s);
+    if (st != hipSuccess) {
+      hip_error(st, "decode upload event");
+      return nullptr;
+    }
+    plan->batch = batch;
+    plan->total_pages = total_pages;
+    plan->num_items = items;
+    plan->chunk_tokens = chunk;
+    plan->items_capacity = items_cap;
+    plan->layout = layout;
+    created.release();
+    return plan;
+  } catch (const std::exception& e) {
+    set_error(e.what());
+    return nullptr;
+  }
+}
+
+extern "C" void mi355x_decode_plan_drop(void* plan) {
+  delete static_cast<DecodePlan*>(plan);
+}
+
+extern "C" uint64_t mi355x_decode_workspace_allocations(const void* plan) {
+  return plan ? static_cast<const DecodePlan*>(plan)->allocations : 0;
+}
+
+// Plan facts: [batch, total_pages, num_items, chunk_tokens, items_capacity, cus].
+extern "C" const char* mi355x_decode_plan_info(const void* plan, int64_t* out6) {
+  if (!plan || !out6) return set_error("mi355x_decode_plan_info: null argument");
+  const auto* p = static_cast<const DecodePlan*>(plan);
+  out6[0] = p->batch;
+  out6[1] = p->total_pages;
+  out6[2] = p->num_items;
+  out6[3] = p->chunk_tokens;
+  out6[4] = p->items_capacity;
+  out6[5] = p->cus;
+  return nullptr;
+}
+
+// Synchronous copy of the plan's page metadata and work list to host memory.
+// Sizes: indptr batch+1, indices total_pages, last_len batch,
+// work 4*num_items, merge 2*batch (any pointer may be NULL).
+extern "C" const char* mi355x_decode_plan_read(const void* plan, int32_t* indptr,
+                                               int32_t* indices, int32_t* last_len,
+                                               int32_t* work, int32_t* merge, void* stream) {
+  if (!plan) return set_error("mi355x_decode_plan_read: null plan");
+  const auto* p = static_cast<const DecodePlan*>(plan);
+  auto s = static_cast<hipStream_t>(stream);
+  const int32_t* ints = static_cast<const int32_t*>(p->ints.ptr);
+  hipError_t st = hipSuccess;
+  auto copy = [&](void* dst, const void* src, size_t bytes) {
+    if (dst && st == hipSuccess && bytes)
+      st = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s);
+  };
+  copy(indptr, ints + p->layout.o_indptr, (p->batch + 1) * 4);
+  copy(indices, p->indices.ptr, p->total_pages * 4);
+  copy(last_len, p->last_len.ptr, p->batch * 4);
+  copy(work, ints + p->layout.o_work, p->num_items * 16);
+  copy(merge, ints + p->layout.o_merge, p->batch * 8);
+  if (st == hipSuccess) st = hipStreamSynchronize(s);
+  return st == hipSuccess ? nullptr : hip_error(st, "mi355x_decode_plan_read");
+}
+
+extern "C" const char* mi355x_decode_run(const void* plan_ptr, const void* q, int64_t q_stride_n,
+                                         int64_t q_stride_h, const void* k_cache,
+                                         const void* v_cache, void* out, int64_t out_stride_n,
+                                         int64_t out_stride_h, int64_t batch, int64_t num_q_heads,
+                                         int64_t num_kv_heads, int64_t page_size, int64_t dtype,
+                                         void* stream) {
+  if (!plan_ptr) return set_error("decode was not prepared");
+  const auto& p = *static_cast<const DecodePlan*>(plan_ptr);
+  if (!q || !k_cache || !v_cache || !out) return set_error("mi355x_decode_run: null pointer");
+  if (num_q_heads != p.num_q_heads || num_kv_heads != p.num_kv_heads ||
+      page_size != p.page_size || dtype != p.dtype || batch != p.batch)
+    return set_error("decode tensors do not match the prepared batch");
+  if (q_stride_h % 8 || q_stride_n % 8 || out_stride_h % 8 || out_stride_n % 8 ||
+      !aligned(q, 16) || !aligned(out, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
+    return set_error("decode requires 16-byte aligned rows");
+  DecodeArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_stride_n = q_stride_n;
+  a.q_stride_h = q_stride_h;
+  a.k_cache = static_cast<const uint16_t*>(k_cache);
+  a.v_cache = static_cast<const uint16_t*>(v_cache);
+  a.out = static_cast<uint16_t*>(out);
+  a.out_stride_n = out_stride_n;
+  a.out_stride_h = out_stride_h;
+  a.ints = static_cast<const int32_t*>(p.ints.ptr);
+  a.o_indptr = static_cast<int32_t>(p.layout.o_indptr);
+  a.o_work = static_cast<int32_t>(p.layout.o_work);
+  a.o_merge = static_cast<int32_t>(p.layout.o_merge);
+  a.indices = static_cast<const int32_t*>(p.indices.ptr);
+  a.partial_o = static_cast<float*>(p.partial_o.ptr);
+  a.partial_lse = static_cast<float*>(p.partial_lse.ptr);
+  a.num_q_heads = static_cast<int32_t>(num_q_heads);
+  a.num_kv_heads = static_cast<int32_t>(num_kv_heads);
+  a.page_size = static_cast<int32_t>(page_size);
+  a.scale_log2 = (1.0f / std::sqrt(static_cast<float>(kHeadDim))) * kLog2e;
+
+  const int waves = static_cast<int>(std::min<int64_t>(num_kv_heads, kMaxWavesPerBlock));
+  const int64_t grid_y = (num_kv_heads + waves - 1) / waves;
+  // Graph plans launch the fixed capacity; surplus workgroups exit at once.
+  const int64_t grid_x = p.graph ? p.items_capacity : p.num_items;
+  const dim3 grid(static_cast<uint32_t>(grid_x), static_cast<uint32_t>(grid_y));
+  const int group = static_cast<int>(num_q_heads / num_kv_heads);
+  auto s = static_cast<hipStream_t>(stream);
+  const bool ok = dtype == 0 ? dispatch_group<0>(a, group, grid, waves, page_size == 1, s)
+                             : dispatch_group<1>(a, group, grid, waves, page_size == 1, s);
+  if (!ok) return set_error("unsupported query group size");
+  if (const char* err = launch_status("decode_kernel")) return err;
+  const bool any_split = p.graph || p.num_items > p.batch;
+  if (any_split) {
+    const dim3 mgrid(static_cast<uint32_t>(batch), static_cast<uint32_t>((num_q_heads + 3) / 4));
+    if (dtype == 0)
+      merge_kernel<0><<<mgrid, dim3(256), 0, s>>>(a, static_cast<int32_t>(batch));
+    else
+      merge_kernel<1><<<mgrid, dim3(256), 0, s>>>(a, static_cast<int32_t>(batch));
+    return launch_status("merge_kernel");
+  }
+  return nullptr;
+}

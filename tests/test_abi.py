@@ -1,0 +1,84 @@
+"""C-ABI library: loads without a GPU, exports every symbol the header declares,
+and its host-only planner satisfies the work-list invariants (CPU only)."""
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+from oracle import plan as oplan
+
+HEADER = ROOT / "include" / "mi355x_attn.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mi355x_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def native():
+    from llm_infer_rust_amd import _native
+    return _native
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for required in ("mi355x_store_kv", "mi355x_rms_norm", "mi355x_add_rms_norm",
+                     "mi355x_qk_norm", "mi355x_decode_prepare", "mi355x_decode_run",
+                     "mi355x_decode_plan_drop"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(native):
+    lib = native.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared but not exported"
+    assert set(native.SIGNATURES) == set(declared_functions())
+    assert lib.mi355x_attn_abi_version() == 1
+
+
+def _schedule(native, lengths, cus=256, hkv=8):
+    lib = native.lib()
+    lens = (ctypes.c_int32 * len(lengths))(*lengths)
+    cap = lib.mi355x_decode_items_capacity(len(lengths), cus, hkv)
+    work = (ctypes.c_int32 * (4 * cap))()
+    merge = (ctypes.c_int32 * (2 * len(lengths)))()
+    chunk = ctypes.c_int64()
+    n = lib.mi355x_decode_schedule(lens, len(lengths), cus, hkv, work, cap, merge,
+                                   ctypes.byref(chunk))
+    return n, list(work)[: 4 * max(n, 0)], list(merge), chunk.value, cap
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_decode_schedule_invariants(native, seed):
+    rng = np.random.default_rng(seed)
+    b = int(rng.choice([1, 3, 64, 256, 700]))
+    lengths = rng.integers(1, 8192, size=b).tolist()
+    n, work, merge, chunk, cap = _schedule(native, lengths)
+    assert 0 < n <= cap
+    oplan.check_work_list(work, merge, lengths)
+    assert chunk % 16 == 0 or chunk == max(lengths)
+
+
+def test_decode_schedule_config2_shape(native):
+    rng = np.random.default_rng(2)
+    lengths = rng.integers(512, 4097, size=64).tolist()
+    n, work, merge, chunk, cap = _schedule(native, lengths)
+    oplan.check_work_list(work, merge, lengths)
+    # enough items to fill 256 CUs, each a bounded slice of the KV
+    assert n >= 512
+    assert chunk >= 128
+
+
+def test_decode_schedule_rejects_bad_input(native):
+    lib = native.lib()
+    lens = (ctypes.c_int32 * 2)(5, 0)
+    work = (ctypes.c_int32 * 64)()
+    merge = (ctypes.c_int32 * 4)()
+    chunk = ctypes.c_int64()
+    assert lib.mi355x_decode_schedule(lens, 2, 256, 8, work, 16, merge, ctypes.byref(chunk)) == -1
+    lens = (ctypes.c_int32 * 1)(10**6)
+    assert lib.mi355x_decode_schedule(lens, 1, 256, 8, work, 1, merge, ctypes.byref(chunk)) == -1
