@@ -140,6 +140,62 @@ int64_t mi355x_decode_schedule(const int32_t* lengths, int64_t batch, int64_t cu
 /* Work-list capacity a plan reserves for `rows` requests. */
 int64_t mi355x_decode_items_capacity(int64_t rows, int64_t cus, int64_t num_kv_heads);
 
+/* ------------------------------------------------------------------------
+ * Causal prefill attention (head_dim 128, q heads per kv head in {1,2,4,8}).
+ * ------------------------------------------------------------------------ */
+
+/* Build or refresh a prefill plan once per forward. q_indptr: device int32
+ * [batch+1] (cu_seqlens_q); block_table: device int32 [batch, columns] with
+ * row stride table_stride (may be NULL when every prefix is 0); q_host /
+ * prefix_host: the scheduler's host snapshots of cu_seqlens_q and
+ * prefix_lens. The plan is paged iff some prefix > 0 and then packs the
+ * reference page metadata over kv length = prefix + extend.
+ * Replaces sglang_flashinfer_prepare_prefill (flashinfer_bridge.cpp:250-253)
+ * and PrefillPlan (flashinfer_plan_run.cu:243-274). */
+void* mi355x_prefill_prepare(void* existing, const int32_t* q_indptr, const int32_t* block_table,
+                             int64_t batch, int64_t columns, int64_t table_stride,
+                             const int32_t* q_host, const int32_t* prefix_host,
+                             int64_t num_q_heads, int64_t num_kv_heads, int64_t page_size,
+                             int64_t dtype, void* stream);
+
+/* out[t, h, :] = causal softmax attention of query row t. q: [total_q,
+ * num_q_heads, 128] with strides (q_sn, q_sh, 1). Ragged plans read k/v as
+ * [total_q, num_kv_heads, 128] with strides (k_sn, k_sh, 1) (packed QKV views
+ * are fine); paged plans read k/v as the contiguous caches [pages,
+ * page_size, num_kv_heads, 128] (pass k_sn = num_kv_heads*128, k_sh = 128).
+ * Rows must be 16-byte aligned. out may be caller-owned static storage.
+ * Replaces sglang_flashinfer_prefill (flashinfer_bridge.cpp:312-314) and
+ * sglang_flashinfer_native_prefill_run (flashinfer_plan_run.cu:331-335). */
+const char* mi355x_prefill_run(const void* plan, const void* q, int64_t q_sn, int64_t q_sh,
+                               const void* k, int64_t k_sn, int64_t k_sh, const void* v,
+                               int64_t v_sn, int64_t v_sh, void* out, int64_t o_sn, int64_t o_sh,
+                               int64_t total_q, int64_t num_q_heads, int64_t num_kv_heads,
+                               int64_t page_size, int64_t dtype, void* stream);
+
+/* Frees a prefill plan after its pending uploads.
+ * Replaces sglang_flashinfer_plan_drop for prefill plans (flashinfer_bridge.cpp:192-199). */
+void mi355x_prefill_plan_drop(void* plan);
+
+/* Workspace (re)allocations made by a prefill plan so far. */
+uint64_t mi355x_prefill_workspace_allocations(const void* plan);
+
+/* Plan facts: out6 = {batch, total_q, paged, num_items, total_pages, 0}.
+ * Introspection; no reference counterpart. */
+const char* mi355x_prefill_plan_info(const void* plan, int64_t* out6);
+
+/* Blocking copy of kv_indptr (batch+1) and, for paged plans, indices
+ * (total_pages) and last_page_len (batch). Introspection for parity tests. */
+const char* mi355x_prefill_plan_read(const void* plan, int32_t* kv_indptr, int32_t* indices,
+                                     int32_t* last_len, void* stream);
+
+/* Host-only prefill work list: 4 ints per item {request, q_begin, kv_head,
+ * head_group}, longest causal horizon first. work may be NULL to count.
+ * Returns the item count or -1. Stands in for FlashInfer's PrefillPlan
+ * tiling (flashinfer_plan_run.cu:243-274). */
+int64_t mi355x_prefill_schedule(const int32_t* q_host, const int32_t* prefix_host, int64_t batch,
+                                int64_t num_q_heads, int64_t num_kv_heads, int32_t* work,
+                                int64_t capacity);
+
 #pragma GCC visibility pop
 
 #ifdef __cplusplus

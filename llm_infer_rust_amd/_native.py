@@ -56,6 +56,18 @@ SIGNATURES: dict[str, tuple] = {
     "mi355x_decode_schedule": (c_i64, [c_void_p, c_i64, c_i64, c_i64, c_void_p, c_i64, c_void_p,
                                        P_i64]),
     "mi355x_decode_items_capacity": (c_i64, [c_i64, c_i64, c_i64]),
+    "mi355x_prefill_prepare": (c_void_p, [c_void_p, c_void_p, c_void_p, c_i64, c_i64, c_i64,
+                                          c_void_p, c_void_p, c_i64, c_i64, c_i64, c_i64,
+                                          c_void_p]),
+    "mi355x_prefill_run": (c_char_p, [c_void_p, c_void_p, c_i64, c_i64, c_void_p, c_i64, c_i64,
+                                      c_void_p, c_i64, c_i64, c_void_p, c_i64, c_i64, c_i64,
+                                      c_i64, c_i64, c_i64, c_i64, c_void_p]),
+    "mi355x_prefill_plan_drop": (None, [c_void_p]),
+    "mi355x_prefill_workspace_allocations": (c_u64, [c_void_p]),
+    "mi355x_prefill_plan_info": (c_char_p, [c_void_p, P_i64]),
+    "mi355x_prefill_plan_read": (c_char_p, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "mi355x_prefill_schedule": (c_i64, [c_void_p, c_void_p, c_i64, c_i64, c_i64, c_void_p,
+                                        c_i64]),
 }
 
 _lock = threading.Lock()

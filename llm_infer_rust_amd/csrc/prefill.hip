@@ -1,0 +1,648 @@
+// Causal GQA prefill attention (head_dim 128) on gfx950 bf16/fp16 MFMA.
+//
+// Reference path this replaces:
+//   plan: sglang_flashinfer_prepare_prefill  src/models/attention/flashinfer_bridge.cpp:250-310
+//         PrefillPlan                        src/models/attention/flashinfer_plan_run.cu:243-274
+//   run:  sglang_flashinfer_prefill          flashinfer_bridge.cpp:312-346
+//         BatchPrefillWith{Ragged,Paged}KVCacheDispatched  flashinfer_plan_run.cu:277-328
+//   math: query i of request r (position prefix_r + i) attends keys j <= prefix_r + i of
+//         the same request, softmax(q k^T / sqrt(128)) v; GQA by contiguous head groups
+//         (backend.rs:1297-1329, 1455-1498 are the libtorch restatement).
+// Mode rule (flashinfer_bridge.cpp:266-273): paged iff some prefix > 0; ragged mode reads
+// K/V straight from the (packed) projection rows, paged mode from the KV cache pages.
+//
+// Kernel design. One workgroup = 4 waves = one (request, query tile, kv head, head group).
+// Each wave owns 32 queries of one q head and keeps, per 64-key tile:
+//   S^T = K Q^T      (v_mfma_f32_32x32x16: A = K rows from LDS, B = Q^T from registers)
+//   O^T += V^T P^T   (A = V^T rows from a transposed LDS copy, B = P^T straight from the
+//                     S^T accumulators, no LDS round trip)
+// In this transposed form each lane holds one query column, so the online-softmax max/sum
+// and the O rescale are per-lane register work plus one cross-half exchange per tile.
+// K/V tiles are double-buffered in LDS (one barrier per tile); the g q heads that share
+// a kv head are processed by the same workgroup so each K/V byte is fetched once per tile.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <memory>
+#include <vector>
+
+#include "common.h"
+
+namespace mi355x {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kTileK = 64;             // keys per tile
+constexpr int kWaves = 4;              // waves per workgroup
+constexpr int kQPerWave = 32;          // queries per wave
+constexpr int kKPitch = kD + 8;        // LDS K row pitch (elements): conflict-free b128 reads
+constexpr int kVPitch = kTileK + 4;    // LDS V^T row pitch (elements): conflict-free b64 reads
+constexpr int kKStage = kTileK * kKPitch;
+constexpr int kVStage = kD * kVPitch;
+constexpr float kLog2e = 1.4426950408889634f;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+template <int DT>
+struct Mfma;
+
+template <>
+struct Mfma<0> {
+  __device__ __forceinline__ static floatx16 run(const uint4& a, const uint4& b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<1> {
+  __device__ __forceinline__ static floatx16 run(const uint4& a, const uint4& b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+};
+
+struct ReqInfo {  // per request, uploaded by the plan
+  int32_t q_start, q_len, prefix, page_base;
+};
+
+struct PrefillArgs {
+  const uint16_t* q;
+  int64_t q_sn, q_sh;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t k_sn, k_sh, v_sn, v_sh;  // ragged strides; paged: slot stride, head stride
+  uint16_t* out;
+  int64_t o_sn, o_sh;
+  const ReqInfo* reqs;
+  const int4* work;  // {request, q_begin, kv_head, head_group}
+  const int32_t* indices;
+  int32_t num_items, num_q_heads, num_kv_heads, page_size;
+  float scale_log2;
+};
+
+__device__ __forceinline__ uint32_t lo16x2(uint32_t a, uint32_t b) {  // {a.lo, b.lo}
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t hi16x2(uint32_t a, uint32_t b) {  // {a.hi, b.hi}
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return static_cast<uint32_t>(Elem<DT>::from_float(a)) |
+         (static_cast<uint32_t>(Elem<DT>::from_float(b)) << 16);
+}
+
+// HPB = q heads per workgroup (1, 2 or 4); BQ = 32 * 4 / HPB queries per workgroup.
+template <int DT, int HPB, bool PAGED>
+__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds_k[2][kKStage];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_v[2][kVStage];
+
+  constexpr int kWavesPerHead = kWaves / HPB;
+  constexpr int kBQ = kQPerWave * kWavesPerHead;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int col = lane & 31;   // query column / MFMA row index
+  const int half = lane >> 5;  // k-half of the MFMA operands
+
+  const int4 w = a.work[blockIdx.x];
+  const ReqInfo rq = a.reqs[w.x];
+  const int q_begin = w.y;
+  const int kvh = w.z;
+  const int group = a.num_q_heads / a.num_kv_heads;
+  const int qh = kvh * group + w.w * HPB + wave / kWavesPerHead;
+  const int wq0 = q_begin + (wave % kWavesPerHead) * kQPerWave;  // wave's first query
+  const int kv_len = rq.prefix + rq.q_len;
+  const int q_hi = min(q_begin + kBQ, rq.q_len);        // workgroup's query end
+  const int keys_needed = min(kv_len, rq.prefix + q_hi);  // causal horizon of the tile
+  const int n_tiles = (keys_needed + kTileK - 1) / kTileK;
+  const bool wave_active = wq0 < rq.q_len;
+  const int wave_last_key = rq.prefix + min(wq0 + kQPerWave, rq.q_len) - 1;
+
+  // Q^T operand: lane holds query (wq0 + col), d = 16 s + 8 half .. +8.
+  uint4 qreg[8];
+  {
+    const int qi = min(wq0 + col, rq.q_len - 1);
+    const uint16_t* qp = a.q + static_cast<int64_t>(rq.q_start + qi) * a.q_sn + qh * a.q_sh;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qreg[s] = ld128(qp + 16 * s + 8 * half);
+  }
+
+  // Global -> register staging of one K/V tile: 4 rows x 16 bytes per thread for each.
+  // K: row = tid/16 + 16 j, d chunk = tid%16. V: keys 4*(tid/16)+j, d chunk = tid%16.
+  const int ld_chunk = tid & 15;
+  const int ld_row = tid >> 4;
+  uint4 kst[4], vst[4];
+  auto key_row = [&](int j, const uint16_t* base, int64_t sn, int64_t sh) -> const uint16_t* {
+    j = min(j, kv_len - 1);
+    int64_t row;
+    if constexpr (PAGED) {
+      row = static_cast<int64_t>(a.indices[rq.page_base + j / a.page_size]) * a.page_size +
+            j % a.page_size;
+    } else {
+      row = rq.q_start + j;
+    }
+    return base + row * sn + kvh * sh + ld_chunk * 8;
+  };
+  auto load_tile = [&](int t) {
+    const int k0 = t * kTileK;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kst[j] = ld128(key_row(k0 + ld_row + 16 * j, a.k, a.k_sn, a.k_sh));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vst[j] = ld128(key_row(k0 + 4 * ld_row + j, a.v, a.v_sn, a.v_sh));
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      st128(&lds_k[buf][(ld_row + 16 * j) * kKPitch + ld_chunk * 8], kst[j]);
+    // Transpose 4 keys x 8 dims into 8 rows of V^T (4 keys each, 8 bytes).
+    const uint32_t w0[4] = {vst[0].x, vst[0].y, vst[0].z, vst[0].w};
+    const uint32_t w1[4] = {vst[1].x, vst[1].y, vst[1].z, vst[1].w};
+    const uint32_t w2[4] = {vst[2].x, vst[2].y, vst[2].z, vst[2].w};
+    const uint32_t w3[4] = {vst[3].x, vst[3].y, vst[3].z, vst[3].w};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int d = ld_chunk * 8 + 2 * p;
+      uint2 even = make_uint2(lo16x2(w0[p], w1[p]), lo16x2(w2[p], w3[p]));
+      uint2 odd = make_uint2(hi16x2(w0[p], w1[p]), hi16x2(w2[p], w3[p]));
+      *reinterpret_cast<uint2*>(&lds_v[buf][d * kVPitch + 4 * ld_row]) = even;
+      *reinterpret_cast<uint2*>(&lds_v[buf][(d + 1) * kVPitch + 4 * ld_row]) = odd;
+    }
+  };
+
+  floatx16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+  float m = -1e30f, l = 0.f;
+  const int my_q = wq0 + col;                // query (local index) of this lane
+  const int my_horizon = rq.prefix + my_q;   // last visible key of this lane's query
+
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < n_tiles; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < n_tiles;
+    if (more) load_tile(t + 1);
+    const int k0 = t * kTileK;
+    if (wave_active && k0 <= wave_last_key) {
+      // S^T for 64 keys: two 32-key blocks.
+      floatx16 s[2];
+#pragma unroll
+      for (int T = 0; T < 2; ++T) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[T][r] = 0.f;
+        const uint16_t* krow = &lds_k[buf][(32 * T + col) * kKPitch + 8 * half];
+#pragma unroll
+        for (int st = 0; st < 8; ++st)
+          s[T] = Mfma<DT>::run(*reinterpret_cast<const uint4*>(krow + 16 * st), qreg[st], s[T]);
+      }
+      const bool need_mask = k0 + kTileK - 1 > rq.prefix + wq0 || k0 + kTileK > kv_len;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float x = s[T][r] * a.scale_log2;
+          if (need_mask) {
+            const int key = k0 + 32 * T + (r >> 2) * 8 + 4 * half + (r & 3);
+            x = (key <= my_horizon && key < kv_len) ? x : -INFINITY;
+          }
+          s[T][r] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      m = m_new;
+      float psum = 0.f;
+      uint4 pb[4];  // P^T operands for the four 16-key k-steps
+#pragma unroll
+      for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          float p[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            p[i] = __builtin_amdgcn_exp2f(s[T][8 * hh + i] - m_new);
+            psum += p[i];
+          }
+          pb[2 * T + hh] = make_uint4(pack2<DT>(p[0], p[1]), pack2<DT>(p[2], p[3]),
+                                      pack2<DT>(p[4], p[5]), pack2<DT>(p[6], p[7]));
+        }
+      l = l * alpha + psum;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      // O^T += V^T P^T. k-step st covers keys 16 st + {4 half + 0..3, 8 + 4 half + 0..3},
+      // the same key order the S^T accumulators hold.
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint16_t* vrow = &lds_v[buf][(32 * db + col) * kVPitch + 4 * half];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * st);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * st + 8);
+          o[db] = Mfma<DT>::run(make_uint4(lo.x, lo.y, hi.x, hi.y), pb[st], o[db]);
+        }
+      }
+    }
+    if (more) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (!wave_active || my_q >= rq.q_len) return;
+  const float lt = l + __shfl_xor(l, 32);
+  const float inv = 1.f / lt;
+  uint16_t* op = a.out + static_cast<int64_t>(rq.q_start + my_q) * a.o_sn + qh * a.o_sh;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = 32 * db + 8 * g4 + 4 * half;
+      const uint2 val = make_uint2(pack2<DT>(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv),
+                                   pack2<DT>(o[db][4 * g4 + 2] * inv, o[db][4 * g4 + 3] * inv));
+      *reinterpret_cast<uint2*>(op + d) = val;
+    }
+}
+
+__global__ __launch_bounds__(256) void pack_prefill_pages(const int32_t* __restrict__ table,
+                                                          const int32_t* __restrict__ indptr,
+                                                          int32_t* __restrict__ indices,
+                                                          int64_t stride) {
+  const int row = blockIdx.x;
+  const int begin = indptr[row];
+  const int pages = indptr[row + 1] - begin;
+  const int32_t* src = table + row * stride;
+  for (int c = threadIdx.x; c < pages; c += blockDim.x) indices[begin + c] = src[c];
+}
+
+struct Buffer {
+  void* ptr = nullptr;
+  size_t capacity = 0;
+  bool pinned = false;
+  hipError_t reserve(size_t bytes, uint64_t& allocations) {
+    if (bytes <= capacity) return hipSuccess;
+    size_t grown = std::max(bytes, capacity ? capacity * 2 : size_t(65536));
+    void* fresh = nullptr;
+    hipError_t st = pinned ? hipHostMalloc(&fresh, grown, hipHostMallocDefault)
+                           : hipMalloc(&fresh, grown);
+    if (st != hipSuccess) return st;
+    release();
+    ptr = fresh;
+    capacity = grown;
+    ++allocations;
+    return hipSuccess;
+  }
+  void release() {
+    if (ptr) {
+      if (pinned)
+        (void)hipHostFree(ptr);
+      else
+        (void)hipFree(ptr);
+    }
+    ptr = nullptr;
+    capacity = 0;
+  }
+  ~Buffer() { release(); }
+};
+
+int heads_per_block(int64_t group) { return group >= 4 ? 4 : static_cast<int>(group); }
+
+}  // namespace
+
+struct PrefillPlan {
+  int device = -1;
+  int64_t num_q_heads = 0, num_kv_heads = 0, page_size = 0, dtype = 0;
+  int64_t batch = 0, total_q = 0, num_items = 0, total_pages = 0;
+  bool paged = false;
+  // Device int32 workspace: [req info 4*B][work 4*items][kv_indptr B+1][last_len B]
+  int64_t o_work = 0, o_indptr = 0, o_last = 0;
+  Buffer ints, indices, staging;
+  hipEvent_t upload_done = nullptr;
+  uint64_t allocations = 0;
+  PrefillPlan() { staging.pinned = true; }
+  ~PrefillPlan() {
+    if (upload_done) {
+      (void)hipEventSynchronize(upload_done);
+      (void)hipEventDestroy(upload_done);
+    }
+  }
+};
+
+}  // namespace mi355x
+
+using namespace mi355x;
+
+// Host-only: the work list a prefill plan launches. Returns the item count (or -1).
+extern "C" int64_t mi355x_prefill_schedule(const int32_t* q_host, const int32_t* prefix_host,
+                                           int64_t batch, int64_t num_q_heads,
+                                           int64_t num_kv_heads, int32_t* work,
+                                           int64_t capacity) {
+  if (!q_host || !prefix_host || batch <= 0 || num_kv_heads <= 0 ||
+      num_q_heads % num_kv_heads != 0)
+    return -1;
+  const int64_t group = num_q_heads / num_kv_heads;
+  const int hpb = heads_per_block(group);
+  if (group % hpb) return -1;
+  const int bq = kQPerWave * (kWaves / hpb);
+  struct Item {
+    int64_t cost;
+    int32_t r, q0, kvh, hg;
+  };
+  std::vector<Item> items;
+  for (int64_t r = 0; r < batch; ++r) {
+    const int64_t q_len = q_host[r + 1] - q_host[r];
+    if (q_len <= 0 || prefix_host[r] < 0) return -1;
+    for (int64_t q0 = 0; q0 < q_len; q0 += bq) {
+      const int64_t horizon = prefix_host[r] + std::min<int64_t>(q0 + bq, q_len);
+      const int64_t cost = (horizon + kTileK - 1) / kTileK;
+      for (int64_t h = 0; h < num_kv_heads; ++h)
+        for (int64_t g = 0; g < group / hpb; ++g)
+          items.push_back({cost, static_cast<int32_t>(r), static_cast<int32_t>(q0),
+                           static_cast<int32_t>(h), static_cast<int32_t>(g)});
+    }
+  }
+  // Longest first: the heavy causal tail starts early and the short tiles fill the gaps.
+  std::stable_sort(items.begin(), items.end(),
+                   [](const Item& x, const Item& y) { return x.cost > y.cost; });
+  const int64_t n = static_cast<int64_t>(items.size());
+  if (work) {
+    if (n > capacity) return -1;
+    for (int64_t i = 0; i < n; ++i) {
+      work[4 * i] = items[i].r;
+      work[4 * i + 1] = items[i].q0;
+      work[4 * i + 2] = items[i].kvh;
+      work[4 * i + 3] = items[i].hg;
+    }
+  }
+  return n;
+}
+
+extern "C" void* mi355x_prefill_prepare(void* existing, const int32_t* q_indptr,
+                                        const int32_t* block_table, int64_t batch,
+                                        int64_t columns, int64_t table_stride,
+                                        const int32_t* q_host, const int32_t* prefix_host,
+                                        int64_t num_q_heads, int64_t num_kv_heads,
+                                        int64_t page_size, int64_t dtype, void* stream) {
+  auto s = static_cast<hipStream_t>(stream);
+  std::unique_ptr<PrefillPlan> created;
+  auto* plan = static_cast<PrefillPlan*>(existing);
+  try {
+    if (!q_indptr || !q_host || !prefix_host || batch <= 0 || page_size <= 0 ||
+        (dtype != 0 && dtype != 1) || num_q_heads <= 0 || num_kv_heads <= 0 ||
+        num_q_heads % num_kv_heads != 0) {
+      set_error("invalid prefill metadata");
+      return nullptr;
+    }
+    const int64_t group = num_q_heads / num_kv_heads;
+    if (group != 1 && group != 2 && group != 4 && group != 8) {
+      set_error("prefill supports 1, 2, 4 or 8 query heads per kv head");
+      return nullptr;
+    }
+    bool paged = false;
+    for (int64_t i = 0; i < batch; ++i) {
+      if (prefix_host[i] < 0 || q_host[i + 1] <= q_host[i] || q_host[0] != 0) {
+        set_error("invalid prefill lengths");
+        return nullptr;
+      }
+      if (block_table &&
+          (int64_t(prefix_host[i]) + q_host[i + 1] - q_host[i] + page_size - 1) / page_size >
+              columns) {
+        set_error("prefill block table is too small");
+        return nullptr;
+      }
+      paged |= prefix_host[i] > 0;
+    }
+    if (paged && (!block_table || columns <= 0 || table_stride < columns)) {
+      set_error("paged prefill requires a block table");
+      return nullptr;
+    }
+    int device = 0;
+    hipError_t st = hipGetDevice(&device);
+    if (st != hipSuccess) {
+      hip_error(st, "hipGetDevice");
+      return nullptr;
+    }
+    if (plan && (plan->device != device || plan->num_q_heads != num_q_heads ||
+                 plan->num_kv_heads != num_kv_heads || plan->page_size != page_size ||
+                 plan->dtype != dtype)) {
+      set_error("prefill geometry changed");
+      return nullptr;
+    }
+    if (!plan) {
+      created = std::make_unique<PrefillPlan>();
+      plan = created.get();
+      plan->device = device;
+      plan->num_q_heads = num_q_heads;
+      plan->num_kv_heads = num_kv_heads;
+      plan->page_size = page_size;
+      plan->dtype = dtype;
+      st = hipEventCreateWithFlags(&plan->upload_done, hipEventDisableTiming);
+      if (st != hipSuccess) {
+        hip_error(st, "hipEventCreate");
+        return nullptr;
+      }
+    }
+    const int64_t n_items =
+        mi355x_prefill_schedule(q_host, prefix_host, batch, num_q_heads, num_kv_heads, nullptr, 0);
+    if (n_items <= 0 || n_items > std::numeric_limits<int32_t>::max()) {
+      set_error("prefill work list is empty or too large");
+      return nullptr;
+    }
+    const int64_t o_work = 4 * batch;
+    const int64_t o_indptr = o_work + 4 * n_items;
+    const int64_t o_last = o_indptr + batch + 1;
+    const int64_t total_ints = o_last + batch;
+    st = hipEventSynchronize(plan->upload_done);
+    if (st != hipSuccess) {
+      hip_error(st, "prefill upload fence");
+      return nullptr;
+    }
+    if ((st = plan->ints.reserve(total_ints * 4, plan->allocations)) != hipSuccess ||
+        (st = plan->staging.reserve(total_ints * 4, plan->allocations)) != hipSuccess) {
+      hip_error(st, "prefill workspace allocation");
+      return nullptr;
+    }
+    int32_t* host = static_cast<int32_t*>(plan->staging.ptr);
+    int64_t total_pages = 0;
+    host[o_indptr] = 0;
+    for (int64_t r = 0; r < batch; ++r) {
+      const int64_t q_len = q_host[r + 1] - q_host[r];
+      const int64_t kv_len = prefix_host[r] + q_len;
+      host[4 * r] = q_host[r];
+      host[4 * r + 1] = static_cast<int32_t>(q_len);
+      host[4 * r + 2] = prefix_host[r];
+      host[4 * r + 3] = static_cast<int32_t>(total_pages);
+      if (paged) {
+        total_pages += (kv_len + page_size - 1) / page_size;
+        if (total_pages > std::numeric_limits<int32_t>::max()) {
+          set_error("prefill page indptr overflow");
+          return nullptr;
+        }
+        host[o_indptr + r + 1] = static_cast<int32_t>(total_pages);
+        host[o_last + r] = static_cast<int32_t>((kv_len - 1) % page_size + 1);
+      } else {
+        host[o_indptr + r + 1] = q_host[r + 1];  // ragged: kv indptr is the q indptr
+        host[o_last + r] = 0;
+      }
+    }
+    mi355x_prefill_schedule(q_host, prefix_host, batch, num_q_heads, num_kv_heads,
+                            host + o_work, n_items);
+    st = hipMemcpyAsync(plan->ints.ptr, host, total_ints * 4, hipMemcpyHostToDevice, s);
+    if (st != hipSuccess) {
+      hip_error(st, "prefill metadata upload");
+      return nullptr;
+    }
+    if (paged) {
+      if ((st = plan->indices.reserve(std::max<int64_t>(total_pages, 1) * 4, plan->allocations)) !=
+          hipSuccess) {
+        hip_error(st, "prefill index allocation");
+        return nullptr;
+      }
+      pack_prefill_pages<<<dim3(static_cast<uint32_t>(batch)), dim3(256), 0, s>>>(
+          block_table, static_cast<const int32_t*>(plan->ints.ptr) + o_indptr,
+          static_cast<int32_t*>(plan->indices.ptr), table_stride);
+      if (launch_status("pack_prefill_pages")) return nullptr;
+    }
+    st = hipEventRecord(plan->upload_done, s);
+    if (st != hipSuccess) {
+      hip_error(st, "prefill upload event");
+      return nullptr;
+    }
+    plan->batch = batch;
+    plan->total_q = q_host[batch];
+    plan->num_items = n_items;
+    plan->total_pages = total_pages;
+    plan->paged = paged;
+    plan->o_work = o_work;
+    plan->o_indptr = o_indptr;
+    plan->o_last = o_last;
+    created.release();
+    return plan;
+  } catch (const std::exception& e) {
+    set_error(e.what());
+    return nullptr;
+  }
+}
+
+extern "C" void mi355x_prefill_plan_drop(void* plan) { delete static_cast<PrefillPlan*>(plan); }
+
+extern "C" uint64_t mi355x_prefill_workspace_allocations(const void* plan) {
+  return plan ? static_cast<const PrefillPlan*>(plan)->allocations : 0;
+}
+
+// Plan facts: out6 = {batch, total_q, paged, num_items, total_pages, 0}.
+extern "C" const char* mi355x_prefill_plan_info(const void* plan, int64_t* out6) {
+  if (!plan || !out6) return set_error("mi355x_prefill_plan_info: null argument");
+  const auto* p = static_cast<const PrefillPlan*>(plan);
+  out6[0] = p->batch;
+  out6[1] = p->total_q;
+  out6[2] = p->paged ? 1 : 0;
+  out6[3] = p->num_items;
+  out6[4] = p->total_pages;
+  out6[5] = 0;
+  return nullptr;
+}
+
+extern "C" const char* mi355x_prefill_plan_read(const void* plan, int32_t* kv_indptr,
+                                                int32_t* indices, int32_t* last_len,
+                                                void* stream) {
+  if (!plan) return set_error("mi355x_prefill_plan_read: null plan");
+  const auto* p = static_cast<const PrefillPlan*>(plan);
+  auto s = static_cast<hipStream_t>(stream);
+  const int32_t* ints = static_cast<const int32_t*>(p->ints.ptr);
+  hipError_t st = hipSuccess;
+  auto copy = [&](void* dst, const void* src, size_t bytes) {
+    if (dst && st == hipSuccess && bytes)
+      st = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s);
+  };
+  copy(kv_indptr, ints + p->o_indptr, (p->batch + 1) * 4);
+  if (p->paged) {
+    copy(indices, p->indices.ptr, p->total_pages * 4);
+    copy(last_len, ints + p->o_last, p->batch * 4);
+  }
+  if (st == hipSuccess) st = hipStreamSynchronize(s);
+  return st == hipSuccess ? nullptr : hip_error(st, "mi355x_prefill_plan_read");
+}
+
+namespace mi355x {
+namespace {
+template <int DT, int HPB>
+void launch_prefill(const PrefillArgs& a, bool paged, hipStream_t s) {
+  const dim3 grid(static_cast<uint32_t>(a.num_items)), block(256);
+  if (paged)
+    prefill_kernel<DT, HPB, true><<<grid, block, 0, s>>>(a);
+  else
+    prefill_kernel<DT, HPB, false><<<grid, block, 0, s>>>(a);
+}
+template <int DT>
+void launch_dt(const PrefillArgs& a, int hpb, bool paged, hipStream_t s) {
+  if (hpb == 1)
+    launch_prefill<DT, 1>(a, paged, s);
+  else if (hpb == 2)
+    launch_prefill<DT, 2>(a, paged, s);
+  else
+    launch_prefill<DT, 4>(a, paged, s);
+}
+}  // namespace
+}  // namespace mi355x
+
+extern "C" const char* mi355x_prefill_run(const void* plan_ptr, const void* q, int64_t q_sn,
+                                          int64_t q_sh, const void* k, int64_t k_sn,
+                                          int64_t k_sh, const void* v, int64_t v_sn,
+                                          int64_t v_sh, void* out, int64_t o_sn, int64_t o_sh,
+                                          int64_t total_q, int64_t num_q_heads,
+                                          int64_t num_kv_heads, int64_t page_size, int64_t dtype,
+                                          void* stream) {
+  if (!plan_ptr) return set_error("prefill was not prepared");
+  const auto& p = *static_cast<const PrefillPlan*>(plan_ptr);
+  if (!q || !k || !v || !out) return set_error("mi355x_prefill_run: null pointer");
+  if (total_q != p.total_q || num_q_heads != p.num_q_heads || num_kv_heads != p.num_kv_heads ||
+      page_size != p.page_size || dtype != p.dtype)
+    return set_error("prefill shape mismatch");
+  if (q_sn % 8 || q_sh % 8 || k_sn % 8 || k_sh % 8 || v_sn % 8 || v_sh % 8 || o_sn % 8 ||
+      o_sh % 8 || !aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 16))
+    return set_error("prefill requires 16-byte aligned rows");
+  PrefillArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_sn = q_sn;
+  a.q_sh = q_sh;
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.k_sn = k_sn;
+  a.k_sh = k_sh;
+  a.v_sn = v_sn;
+  a.v_sh = v_sh;
+  a.out = static_cast<uint16_t*>(out);
+  a.o_sn = o_sn;
+  a.o_sh = o_sh;
+  const int32_t* ints = static_cast<const int32_t*>(p.ints.ptr);
+  a.reqs = reinterpret_cast<const ReqInfo*>(ints);
+  a.work = reinterpret_cast<const int4*>(ints + p.o_work);
+  a.indices = static_cast<const int32_t*>(p.indices.ptr);
+  a.num_items = static_cast<int32_t>(p.num_items);
+  a.num_q_heads = static_cast<int32_t>(num_q_heads);
+  a.num_kv_heads = static_cast<int32_t>(num_kv_heads);
+  a.page_size = static_cast<int32_t>(p.paged ? page_size : 1);
+  a.scale_log2 = (1.0f / std::sqrt(static_cast<float>(kD))) * kLog2e;
+  const int hpb = heads_per_block(num_q_heads / num_kv_heads);
+  auto s = static_cast<hipStream_t>(stream);
+  if (dtype == 0)
+    launch_dt<0>(a, hpb, p.paged, s);
+  else
+    launch_dt<1>(a, hpb, p.paged, s);
+  return launch_status("prefill_kernel");
+}

@@ -41,12 +41,13 @@ def attention_against_cache(q: np.ndarray, k: np.ndarray, v: np.ndarray, prefix_
     vv = np.repeat(v, group, axis=1)
     if blocked is None:
         blocked = blocked_attention_mask(lq, k.shape[0], prefix_len)
-    scores = np.einsum("qhd,khd->hqk", q, kk) * (1.0 / math.sqrt(d))
+    # [H, Lq, D] @ [H, D, Lk] through BLAS matmul
+    scores = np.matmul(q.transpose(1, 0, 2), kk.transpose(1, 2, 0)) * (1.0 / math.sqrt(d))
     scores = np.where(blocked[None, :, :], -np.inf, scores)
     mx = scores.max(axis=-1, keepdims=True)
     p = np.exp(scores - mx)
     p /= p.sum(axis=-1, keepdims=True)
-    return np.einsum("hqk,khd->qhd", p, vv)
+    return np.matmul(p, vv.transpose(1, 0, 2)).transpose(1, 0, 2)
 
 
 def slots_of(table_row: np.ndarray, length: int, page_size: int) -> np.ndarray:

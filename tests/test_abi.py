@@ -28,7 +28,8 @@ def test_header_declares_the_boundary():
     names = declared_functions()
     for required in ("mi355x_store_kv", "mi355x_rms_norm", "mi355x_add_rms_norm",
                      "mi355x_qk_norm", "mi355x_decode_prepare", "mi355x_decode_run",
-                     "mi355x_decode_plan_drop"):
+                     "mi355x_decode_plan_drop", "mi355x_prefill_prepare", "mi355x_prefill_run",
+                     "mi355x_prefill_plan_drop"):
         assert required in names
 
 

@@ -1,0 +1,186 @@
+"""Ragged and paged causal prefill through the C ABI against the oracle.
+
+Tolerance (every case): max-abs <= 2e-2 and cosine similarity > 0.9999 against
+the float64 oracle on the same rounded inputs (the reference itself allows
+0.03125, backend.rs:1846). Paged page metadata is compared bit-exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+from llm_infer_rust_amd.backend import (Attention, AttentionMetadata, AttentionSpec, BatchPhase,
+                                        ModelError)
+from llm_infer_rust_amd.kv_cache import BaseAttention
+from oracle import attention as oatt
+from oracle import plan as oplan
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MIN_COS = 0.9999
+
+
+def f32(t):
+    return t.float().cpu().numpy()
+
+
+def assert_close(got, want, what=""):
+    got = np.asarray(got, np.float64).ravel()
+    want = np.asarray(want, np.float64).ravel()
+    err = float(np.abs(got - want).max())
+    cs = float(got @ want / (np.linalg.norm(got) * np.linalg.norm(want) + 1e-30))
+    assert err <= MAX_ABS and cs > MIN_COS, f"{what} max_abs={err} cos={cs}"
+
+
+def randn(shape, g, dtype, gpu):
+    return torch.randn(*shape, generator=g).to(dtype).to(gpu)
+
+
+def make(gpu, hq, hkv, page, dtype):
+    attn = Attention.new("mi355x", AttentionSpec(hq, hkv, 128, dtype, gpu))
+    attn.bind_cache_layout(page)
+    return attn
+
+
+def meta_for(gpu, bounds, prefixes, table):
+    return AttentionMetadata(BatchPhase.PREFILL,
+                             cu_seqlens_q=torch.tensor(bounds, dtype=torch.int32, device=gpu),
+                             prefix_lens=torch.tensor(prefixes, dtype=torch.int32, device=gpu),
+                             block_table=table)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_reference_ragged_and_cached_cases(gpu, fixtures, dtype):
+    fx = fixtures["prefill_cases"]
+    g = torch.Generator().manual_seed(5)
+    attn = make(gpu, 16, 8, fx["page_size"], dtype)
+    kc = randn(fx["cache_shape"], g, dtype, gpu)
+    vc = randn(fx["cache_shape"], g, dtype, gpu)
+    cache = BaseAttention()
+    cache.bind_kv_cache(kc, vc)
+    table = torch.arange(64, dtype=torch.int32, device=gpu).view(2, 32)
+    for lengths, prefixes in fx["cases"]:
+        bounds = [0, lengths[0], lengths[0] + lengths[1]]
+        n = bounds[-1]
+        packed = randn((n, fx["packed_width"]), g, dtype, gpu)
+        q = packed[:, :2048].view(-1, 16, 128)
+        k = packed[:, 2048:3072].view(-1, 8, 128)
+        v = packed[:, 3072:].view(-1, 8, 128)
+        batch = attn.prepare(meta_for(gpu, bounds, prefixes, table), n)
+        plan = batch.plan.plan
+        paged = any(p > 0 for p in prefixes)
+        assert plan.paged == paged
+        actual = batch.forward(q, k, v, cache)
+        storage = torch.full((n + 3, 2048), 99.0, dtype=dtype, device=gpu)
+        target = storage[:n]
+        ptr = target.data_ptr()
+        batch.forward_into(q, k, v, cache, target)
+        assert target.data_ptr() == ptr and torch.equal(actual, target)
+        assert bool((storage[n:] == 99.0).all())
+        if paged:
+            want = oatt.prefill_with_cache(f32(q), f32(kc), f32(vc), table.cpu().numpy(), bounds,
+                                           prefixes, fx["page_size"])
+            md = plan.read_metadata()
+            _, indptr, indices, last = oplan.prefill_page_metadata(
+                table.cpu().numpy(), bounds, prefixes, fx["page_size"])
+            assert md["kv_indptr"] == indptr.tolist()
+            assert md["indices"] == indices.tolist()
+            assert md["last_page_len"] == last.tolist()
+        else:
+            want = oatt.prefill_ragged(f32(q), f32(k), f32(v), bounds)
+        assert_close(f32(actual).reshape(want.shape), want, f"{lengths} {prefixes} {dtype}")
+        del batch
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 16), (32, 8), (64, 8), (4, 2)])
+def test_ragged_gqa_groups(gpu, hq, hkv):
+    g = torch.Generator().manual_seed(hq + hkv)
+    bounds = [0, 1, 70, 200, 333, 334]
+    n = bounds[-1]
+    q = randn((n, hq, 128), g, torch.bfloat16, gpu)
+    k = randn((n, hkv, 128), g, torch.bfloat16, gpu)
+    v = randn((n, hkv, 128), g, torch.bfloat16, gpu)
+    attn = make(gpu, hq, hkv, 16, torch.bfloat16)
+    table = torch.zeros(len(bounds) - 1, 32, dtype=torch.int32, device=gpu)
+    batch = attn.prepare(meta_for(gpu, bounds, [0] * (len(bounds) - 1), table), n)
+    out = batch.forward(q, k, v, BaseAttention())
+    want = oatt.prefill_ragged(f32(q), f32(k), f32(v), bounds)
+    assert_close(f32(out).reshape(want.shape), want, f"hq={hq} hkv={hkv}")
+
+
+def test_config3_ragged_shape(gpu):
+    """8 sequences, lengths U[256,2048], Hq16/Hkv8, packed QKV stride 4096."""
+    rng = np.random.default_rng(3)
+    g = torch.Generator().manual_seed(3)
+    lens = rng.integers(256, 2049, size=8)
+    bounds = [0] + np.cumsum(lens).tolist()
+    n = bounds[-1]
+    packed = randn((n, 4096), g, torch.bfloat16, gpu)
+    q = packed[:, :2048].view(-1, 16, 128)
+    k = packed[:, 2048:3072].view(-1, 8, 128)
+    v = packed[:, 3072:].view(-1, 8, 128)
+    attn = make(gpu, 16, 8, 16, torch.bfloat16)
+    table = torch.zeros(8, 2048 // 16, dtype=torch.int32, device=gpu)
+    batch = attn.prepare(meta_for(gpu, bounds, [0] * 8, table), n)
+    out = batch.forward(q, k, v, BaseAttention())
+    want = oatt.prefill_ragged(f32(q), f32(k), f32(v), bounds)
+    assert_close(f32(out).reshape(want.shape), want, "config3")
+
+
+def test_config4_paged_shape_sampled_rows(gpu):
+    """16 requests, prefix U[1024,8192] over a random page permutation, extend U[64,512],
+    Hq32/Hkv8, page 16. The oracle checks 12 query rows per request (first, last, random)."""
+    rng = np.random.default_rng(4)
+    g = torch.Generator().manual_seed(4)
+    page = 16
+    pref = rng.integers(1024, 8193, size=16)
+    ext = rng.integers(64, 513, size=16)
+    bounds = [0] + np.cumsum(ext).tolist()
+    pages_per = (pref + ext + page - 1) // page
+    cols = int(pages_per.max())
+    total_pages = int(pages_per.sum())
+    pool = total_pages + 1
+    perm = rng.permutation(pool - 1) + 1
+    table = np.zeros((16, cols), np.int32)
+    off = 0
+    for r in range(16):
+        table[r, : pages_per[r]] = perm[off: off + pages_per[r]]
+        off += pages_per[r]
+    kc = randn((pool, page, 8, 128), g, torch.bfloat16, gpu)
+    vc = randn((pool, page, 8, 128), g, torch.bfloat16, gpu)
+    n = bounds[-1]
+    q = randn((n, 32, 128), g, torch.bfloat16, gpu)
+    attn = make(gpu, 32, 8, page, torch.bfloat16)
+    cache = BaseAttention()
+    cache.bind_kv_cache(kc, vc)
+    tdev = torch.from_numpy(table).to(gpu)
+    batch = attn.prepare(meta_for(gpu, bounds, pref.tolist(), tdev), n)
+    assert batch.plan.plan.paged
+    out = f32(batch.forward(q, q, q, cache)).reshape(n, 32, 128)
+    kcf, vcf, qf = f32(kc), f32(vc), f32(q)
+    flat_k = kcf.reshape(-1, 8, 128)
+    flat_v = vcf.reshape(-1, 8, 128)
+    for r in range(16):
+        e = int(ext[r])
+        rows = sorted(set([0, e - 1] + rng.integers(0, e, size=10).tolist()))
+        for i in rows:
+            horizon = int(pref[r]) + i + 1
+            slots = oatt.slots_of(table[r], horizon, page)
+            want = oatt.attention_against_cache(qf[bounds[r] + i: bounds[r] + i + 1],
+                                                flat_k[slots], flat_v[slots], horizon - 1, 32, 8)
+            assert_close(out[bounds[r] + i], want[0], f"req={r} row={i}")
+
+
+def test_prefill_plan_reuse_and_errors(gpu):
+    attn = make(gpu, 16, 8, 16, torch.bfloat16)
+    table = torch.arange(64, dtype=torch.int32, device=gpu).view(2, 32)
+    batch = attn.prepare(meta_for(gpu, [0, 17, 18], [0, 0], table), 18)
+    handle = batch.plan.plan.handle
+    with pytest.raises(ModelError, match="still in use"):
+        attn.prepare(meta_for(gpu, [0, 17, 18], [0, 0], table), 18)
+    del batch
+    batch = attn.prepare(meta_for(gpu, [0, 1, 18], [255, 16], table), 18)
+    assert batch.plan.plan.handle == handle and batch.plan.plan.paged
+    del batch
+    with pytest.raises(ModelError, match="too small"):
+        attn.prepare(meta_for(gpu, [0, 1, 2], [600, 0], table), 2)
