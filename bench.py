@@ -26,18 +26,21 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
 METRIC = "decode-attn HBM GB/s (% peak); prefill MFMA util; output tok/s Qwen3-8B"
 
 
 def parse_args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--steps", type=int, default=2000)
+    p.add_argument("--warmup", type=int, default=500)
     p.add_argument("--seed", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-requests", type=int, default=16,
                    help="requests in the bounded CPU-baseline sample")
+    p.add_argument("--decode-only", action="store_true",
+                   help="skip the prefill and norm measurements")
     return p.parse_args()
 
 
@@ -108,6 +111,114 @@ def cpu_baseline(w, requests: int):
     return {"value": nbytes / sec / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{len(idx)} of 64 requests ({sum(lens)} KV tokens), libtorch fp32 CPU "
                       "decode_with_cache restatement, median of 5"}
+
+
+def _event_time_ms(fn, reps: int) -> float:
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def prefill_sections(dev, reps: int) -> dict:
+    """cfg3 ragged causal prefill and cfg4 paged prefill over a cached prefix (bf16 MFMA)."""
+    from llm_infer_rust_amd.backend import (AttentionMetadata, AttentionSpec, BatchPhase,
+                                            PrefillMetadata)
+    from llm_infer_rust_amd.prefill import prepare_prefill_plan, run_prefill
+
+    out = {}
+    # cfg3: 8 sequences, L ~ U[256, 2048], Hq16/Hkv8, packed QKV stride 4096.
+    g = torch.Generator().manual_seed(3)
+    lens = torch.randint(256, 2049, (8,), generator=g)
+    bounds = [0] + torch.cumsum(lens, 0).tolist()
+    n = bounds[-1]
+    gd = torch.Generator(device=dev).manual_seed(3)
+    packed = torch.randn(n, 4096, generator=gd, device=dev, dtype=torch.bfloat16)
+    q = packed[:, :2048].view(-1, 16, 128)
+    k = packed[:, 2048:3072].view(-1, 8, 128)
+    v = packed[:, 3072:].view(-1, 8, 128)
+    meta = AttentionMetadata(BatchPhase.PREFILL,
+                             cu_seqlens_q=torch.tensor(bounds, dtype=torch.int32, device=dev),
+                             prefix_lens=torch.zeros(8, dtype=torch.int32, device=dev),
+                             block_table=torch.zeros(8, 128, dtype=torch.int32, device=dev))
+    spec = AttentionSpec(16, 8, 128, torch.bfloat16, dev)
+    plan = prepare_prefill_plan(None, meta, PrefillMetadata(bounds, [0] * 8), spec, 16)
+    o = torch.empty_like(q)
+    ms = _event_time_ms(lambda: run_prefill(plan, q, k, v, o), reps)
+    flops = 4 * 16 * 128 * sum(int(x) * (int(x) + 1) // 2 for x in lens)
+    tf = flops / (ms * 1e-3) / 1e12
+    out["prefill_ragged_cfg3"] = {"us": round(ms * 1e3, 2), "flops": flops,
+                                  "TFLOP/s": round(tf, 2),
+                                  "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                                  "tokens": n}
+    del plan
+    # cfg4: 16 requests, prefix ~ U[1024, 8192], extend ~ U[64, 512], Hq32/Hkv8, page 16.
+    g = torch.Generator().manual_seed(4)
+    page = 16
+    pref = torch.randint(1024, 8193, (16,), generator=g)
+    ext = torch.randint(64, 513, (16,), generator=g)
+    pages_per = (pref + ext + page - 1) // page
+    cols = int(pages_per.max())
+    pool = int(pages_per.sum()) + 1
+    perm = torch.randperm(pool - 1, generator=g) + 1
+    table = torch.zeros(16, cols, dtype=torch.int32)
+    off = 0
+    for r in range(16):
+        m = int(pages_per[r])
+        table[r, :m] = perm[off: off + m].to(torch.int32)
+        off += m
+    kc = torch.randn(pool, page, 8, 128, generator=gd, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn(pool, page, 8, 128, generator=gd, device=dev, dtype=torch.bfloat16)
+    bounds = [0] + torch.cumsum(ext, 0).tolist()
+    n = bounds[-1]
+    q = torch.randn(n, 32, 128, generator=gd, device=dev, dtype=torch.bfloat16)
+    meta = AttentionMetadata(BatchPhase.PREFILL,
+                             cu_seqlens_q=torch.tensor(bounds, dtype=torch.int32, device=dev),
+                             prefix_lens=pref.to(torch.int32).to(dev),
+                             block_table=table.to(dev))
+    spec = AttentionSpec(32, 8, 128, torch.bfloat16, dev)
+    plan = prepare_prefill_plan(None, meta, PrefillMetadata(bounds, pref.tolist()), spec, page)
+    o = torch.empty_like(q)
+    ms = _event_time_ms(lambda: run_prefill(plan, q, kc, vc, o), reps)
+    flops = 4 * 32 * 128 * sum(int(e) * int(p) + int(e) * (int(e) + 1) // 2
+                               for e, p in zip(ext, pref))
+    tf = flops / (ms * 1e-3) / 1e12
+    out["prefill_paged_cfg4"] = {"us": round(ms * 1e3, 2), "flops": flops,
+                                 "TFLOP/s": round(tf, 2),
+                                 "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                                 "extend_tokens": n, "prefix_tokens": int(pref.sum())}
+    return out
+
+
+def norm_sections(dev, reps: int) -> dict:
+    """cfg3 norms on 8192 x 1024 hidden rows and the 8192-token packed QKV (HBM-bound)."""
+    from llm_infer_rust_amd import ops
+
+    gd = torch.Generator(device=dev).manual_seed(33)
+    x = torch.randn(8192, 1024, generator=gd, device=dev, dtype=torch.bfloat16)
+    r = torch.randn(8192, 1024, generator=gd, device=dev, dtype=torch.bfloat16)
+    w = torch.rand(1024, generator=gd, device=dev).add_(0.5).to(torch.bfloat16)
+    packed = torch.randn(8192, 4096, generator=gd, device=dev, dtype=torch.bfloat16)
+    q = packed[:, :2048].view(-1, 16, 128)
+    k = packed[:, 2048:3072].view(-1, 8, 128)
+    qw = torch.rand(128, generator=gd, device=dev).add_(0.5).to(torch.bfloat16)
+    kw = torch.rand(128, generator=gd, device=dev).add_(0.5).to(torch.bfloat16)
+    res = {}
+    for name, fn, nbytes in (
+            ("rms_norm", lambda: ops.rms_norm(x, w, 1e-6), 2 * 8192 * 1024 * 2),
+            ("add_rms_norm", lambda: ops.add_rms_norm(x, r, w, 1e-6), 4 * 8192 * 1024 * 2),
+            ("qk_norm", lambda: ops.qk_norm(q, k, qw, kw, 1e-6), 2 * 8192 * 24 * 128 * 2)):
+        ms = _event_time_ms(fn, reps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return res
 
 
 def main():
@@ -198,6 +309,9 @@ def main():
                      "GB/s": round(sbytes / (store_ms * 1e-3) / 1e9, 2)},
         "plan_prepare_ms": round(plan_ms, 3),
     }
+    if not args.decode_only:
+        result["prefill"] = prefill_sections(dev, reps)
+        result["norms"] = norm_sections(dev, reps)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_requests)
     print(json.dumps(result))

@@ -31,23 +31,31 @@ inline bool aligned(const void* p, uintptr_t a) {
 }
 
 // ----------------------------------------------------------------------------
-// 16-bit float conversions. bf16 -> f32 is exact (shift); f32 -> bf16 rounds
-// to nearest-even with NaN kept quiet, which is what torch's CPU and GPU
-// casts do, so residual write-backs compare bit-exactly.
+// 16-bit float conversions. bf16 -> f32 is exact (shift); f32 -> bf16/f16
+// rounds to nearest-even, which is what torch's CPU and GPU casts do, so
+// residual write-backs compare bit-exactly.
 // ----------------------------------------------------------------------------
 template <int DT>
 struct Elem;
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_vec_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_vec_t __attribute__((ext_vector_type(2)));
+
+// Conversions use the gfx950 hardware converts (v_cvt_pk_bf16_f32 /
+// v_cvt_f16_f32), which round to nearest-even.
 template <>
 struct Elem<0> {  // bfloat16
   __device__ __forceinline__ static float to_float(uint16_t h) {
     return __uint_as_float(static_cast<uint32_t>(h) << 16);
   }
   __device__ __forceinline__ static uint16_t from_float(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+  }
+  // Two floats -> one packed word {lo = a, hi = b}.
+  __device__ __forceinline__ static uint32_t pack2(float a, float b) {
+    const f32x2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_vec_t));
   }
 };
 
@@ -60,6 +68,10 @@ struct Elem<1> {  // float16
   __device__ __forceinline__ static uint16_t from_float(float f) {
     _Float16 v = static_cast<_Float16>(f);  // round-to-nearest-even
     return __builtin_bit_cast(uint16_t, v);
+  }
+  __device__ __forceinline__ static uint32_t pack2(float a, float b) {
+    const f32x2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_vec_t));
   }
 };
 
@@ -76,13 +88,8 @@ __device__ __forceinline__ void unpack8(const uint4& w, float (&f)[8]) {
 
 template <int DT>
 __device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
-  uint32_t words[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    words[i] = static_cast<uint32_t>(Elem<DT>::from_float(f[2 * i])) |
-               (static_cast<uint32_t>(Elem<DT>::from_float(f[2 * i + 1])) << 16);
-  }
-  return make_uint4(words[0], words[1], words[2], words[3]);
+  return make_uint4(Elem<DT>::pack2(f[0], f[1]), Elem<DT>::pack2(f[2], f[3]),
+                    Elem<DT>::pack2(f[4], f[5]), Elem<DT>::pack2(f[6], f[7]));
 }
 
 // ----------------------------------------------------------------------------
@@ -116,6 +123,20 @@ __device__ __forceinline__ float row16_max(float x) {
   x = fmaxf(x, dpp<kDppRowHalfMirror>(x));
   x = fmaxf(x, dpp<kDppRowMirror>(x));
   return x;
+}
+
+// N independent 16-lane sums advanced in lockstep, so consecutive DPP ops never
+// read the register the previous op just wrote (no hazard wait states).
+template <int N>
+__device__ __forceinline__ void row16_sum_n(float (&x)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) x[i] += dpp<kDppQuadSwap1>(x[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) x[i] += dpp<kDppQuadSwap2>(x[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) x[i] += dpp<kDppRowHalfMirror>(x[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) x[i] += dpp<kDppRowMirror>(x[i]);
 }
 
 // Sum over the whole 64-lane wave; all lanes receive the total.

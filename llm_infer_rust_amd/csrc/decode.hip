@@ -1,5 +1,5 @@
 // Paged decode attention for gfx950: per-forward plan (page metadata + split-KV
-// work list) and the decode / merge kernels.
+// work list), the decode kernel and the split-KV merge kernel.
 //
 // Reference path this replaces:
 //   plan:  sglang_flashinfer_prepare   src/models/attention/flashinfer_bridge.cpp:61-185
@@ -22,9 +22,13 @@
 // item for up to 8 KV heads (one wave per KV head), so the 2 KiB K row and the
 // 2 KiB V row of a page-size-1 slot are fetched by one workgroup at the same
 // time. A request that fits one chunk writes its output directly; others
-// write normalised fp32 partials + log2-sum-exp, combined by the merge kernel.
+// write normalised fp32 partials + log2-sum-exp that a small merge kernel
+// combines. (Merging inside the last-arriving workgroup needs an agent-scope
+// release per workgroup, i.e. an L2 write-back on every XCD, and measured ~5x
+// slower than the extra launch.)
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <memory>
@@ -37,7 +41,7 @@ namespace {
 
 constexpr int kHeadDim = 128;
 constexpr int kTokensPerLaneGroup = 4;  // tokens per 16-lane group per loop trip
-constexpr int kTileTokens = 4 * kTokensPerLaneGroup;
+constexpr int kTileTokens = 32;  // chunk granularity: a multiple of every tile size (4 * U)
 constexpr int kMaxWavesPerBlock = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -131,11 +135,33 @@ namespace {
 // ---------------------------------------------------------------------------
 // Host planner: split-KV work list. Pure host code.
 // ---------------------------------------------------------------------------
+// Resident waves per CU the split-KV schedule aims to fill. Override with
+// MI355X_DECODE_WAVES_PER_CU (tuning knob; read once).
+int64_t waves_per_cu_target() {
+  static const int64_t value = [] {
+    const char* env = std::getenv("MI355X_DECODE_WAVES_PER_CU");
+    const long v = env ? std::strtol(env, nullptr, 10) : 0;
+    return v > 0 ? static_cast<int64_t>(v) : int64_t(32);
+  }();
+  return value;
+}
+
+// Waves (= kv heads) per decode workgroup. Override with
+// MI355X_DECODE_WAVES_PER_BLOCK (1..8; tuning knob, read once).
+int64_t waves_per_block(int64_t num_kv_heads) {
+  static const int64_t cap = [] {
+    const char* env = std::getenv("MI355X_DECODE_WAVES_PER_BLOCK");
+    const long v = env ? std::strtol(env, nullptr, 10) : 0;
+    return (v >= 1 && v <= kMaxWavesPerBlock) ? static_cast<int64_t>(v)
+                                              : static_cast<int64_t>(kMaxWavesPerBlock);
+  }();
+  return std::min<int64_t>(num_kv_heads, cap);
+}
+
 int64_t target_items_for(int64_t cus, int64_t num_kv_heads) {
-  const int64_t waves = std::min<int64_t>(num_kv_heads, kMaxWavesPerBlock);
+  const int64_t waves = waves_per_block(num_kv_heads);
   const int64_t grid_y = (num_kv_heads + waves - 1) / waves;
-  // About 32 resident waves per CU; keep ~1 full round of workgroups.
-  const int64_t per_cu = std::max<int64_t>(1, 32 / waves);
+  const int64_t per_cu = std::max<int64_t>(1, waves_per_cu_target() / waves);
   return std::max<int64_t>(1, cus * per_cu / grid_y);
 }
 
@@ -244,26 +270,123 @@ __device__ __forceinline__ float dot8(const uint4& a, const uint4& b) {
   return s;
 }
 
-template <int DT, int G, bool P1>
+template <bool P1>
+__device__ __forceinline__ int64_t slot_of(const int32_t* pages, int t, int page_size) {
+  if constexpr (P1) {
+    return pages[t];
+  } else {
+    return static_cast<int64_t>(pages[t / page_size]) * page_size + t % page_size;
+  }
+}
+
+// {a.lo16, b.lo16} and {a.hi16, b.hi16} (v_perm_b32).
+__device__ __forceinline__ uint32_t pair_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// Online-softmax update of one lane group with U tokens of K/V (U even).
+// QK: v_dot2 on packed q/k words + a 16-lane DPP sum. PV: the V words of two
+// tokens are re-paired per dim (v_perm) and accumulated with one v_dot2 per
+// dim against the packed pair of their probabilities, so V is never unpacked.
+template <int DT, int G, int U>
+__device__ __forceinline__ void consume(const uint4 (&qv)[G], const uint4 (&kr)[U],
+                                       const uint4 (&vr)[U], const bool (&valid)[U],
+                                       float scale_log2, float (&m)[G], float (&l)[G],
+                                       float (&o)[G][8]) {
+  static_assert(U % 2 == 0, "tokens are consumed in pairs");
+  // Per dim pair (2k, 2k+1) and token pair: words {a[2k], b[2k]}, {a[2k+1], b[2k+1]}.
+  uint32_t vp[U / 2][8];
+#pragma unroll
+  for (int u = 0; u < U; u += 2) {
+    const uint32_t a[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+    const uint32_t b[4] = {vr[u + 1].x, vr[u + 1].y, vr[u + 1].z, vr[u + 1].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      vp[u / 2][2 * k] = pair_lo(a[k], b[k]);
+      vp[u / 2][2 * k + 1] = pair_hi(a[k], b[k]);
+    }
+  }
+  float sc[G * U];
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+    for (int u = 0; u < U; ++u) sc[gi * U + u] = dot8<DT>(qv[gi], kr[u]);
+  row16_sum_n<G * U>(sc);
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    float s[U];
+    float mx = m[gi];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      s[u] = valid[u] ? sc[gi * U + u] * scale_log2 : -INFINITY;
+      mx = fmaxf(mx, s[u]);
+    }
+    const float corr = __builtin_amdgcn_exp2f(m[gi] - mx);
+    m[gi] = mx;
+    float psum = 0.f;
+    uint32_t pp[U / 2];
+#pragma unroll
+    for (int u = 0; u < U; u += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(s[u] - mx);
+      const float p1 = __builtin_amdgcn_exp2f(s[u + 1] - mx);
+      psum += p0 + p1;
+      pp[u / 2] = Elem<DT>::pack2(p0, p1);
+    }
+    l[gi] = l[gi] * corr + psum;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float acc = o[gi][i] * corr;
+#pragma unroll
+      for (int u = 0; u < U / 2; ++u) acc = dot2<DT>(vp[u][i], pp[u], acc);
+      o[gi][i] = acc;
+    }
+  }
+}
+
+// Element offset of token t's row: slot * row_elems as one 32x32->64 multiply
+// (slots < 2^31, rows < 2^32 elements).
+template <bool P1>
+__device__ __forceinline__ uint64_t slot_offset(const int32_t* pages, int t, int page_size,
+                                                uint32_t row_elems) {
+  uint32_t slot;
+  if constexpr (P1) {
+    slot = static_cast<uint32_t>(pages[t]);
+  } else {
+    slot = static_cast<uint32_t>(pages[t / page_size]) * static_cast<uint32_t>(page_size) +
+           static_cast<uint32_t>(t % page_size);
+  }
+  return static_cast<uint64_t>(slot) * row_elems;
+}
+
+// One workgroup = one (request, token chunk) work item; wave w handles kv head
+// blockIdx.y * waves + w and its G query heads. Inside a wave, lane group
+// grp = lane / 16 takes tokens t0 + 4 u + grp (u < U) and each lane owns 8 of
+// the 128 dims. Slot offsets of the next tile are loaded while the current
+// tile's K/V rows are in flight.
+template <int DT, int G, bool P1, int U>
 __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
+  constexpr int kTile = 4 * U;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int h = blockIdx.y * (blockDim.x >> 6) + wave;  // kv head
+  const int waves = blockDim.x >> 6;
+  const int h = blockIdx.y * waves + wave;  // kv head
   const int item = blockIdx.x;
-  if (h >= a.num_kv_heads || item >= a.ints[0]) return;  // uniform per wave
+  if (item >= a.ints[0] || h >= a.num_kv_heads) return;  // graph plans launch a fixed capacity
 
   const int4 w = reinterpret_cast<const int4*>(a.ints + a.o_work)[item];
   const int req = w.x, beg = w.y, end = w.z, pslot = w.w;
   const int grp = lane >> 4, sub = lane & 15;
 
-  // Query rows of the G heads that share kv head h, kept packed (8 x 16-bit).
   uint4 qv[G];
 #pragma unroll
   for (int gi = 0; gi < G; ++gi)
     qv[gi] = ld128(a.q + req * a.q_stride_n + (h * G + gi) * a.q_stride_h + sub * 8);
 
   const int32_t* pages = a.indices + a.ints[a.o_indptr + req];
-  const int64_t row_elems = static_cast<int64_t>(a.num_kv_heads) * kHeadDim;
+  const uint32_t row_elems = static_cast<uint32_t>(a.num_kv_heads) * kHeadDim;
   const uint16_t* kbase = a.k_cache + h * kHeadDim + sub * 8;
   const uint16_t* vbase = a.v_cache + h * kHeadDim + sub * 8;
 
@@ -276,48 +399,27 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
     for (int i = 0; i < 8; ++i) o[gi][i] = 0.f;
   }
 
-  for (int t0 = beg; t0 < end; t0 += kTileTokens) {
-    uint4 kr[kTokensPerLaneGroup], vr[kTokensPerLaneGroup];
-    bool valid[kTokensPerLaneGroup];
+  uint64_t off[U];
 #pragma unroll
-    for (int u = 0; u < kTokensPerLaneGroup; ++u) {
-      const int t = t0 + u * 4 + grp;
-      valid[u] = t < end;
-      const int tt = valid[u] ? t : beg;
-      int64_t slot;
-      if constexpr (P1) {
-        slot = pages[tt];
-      } else {
-        slot = static_cast<int64_t>(pages[tt / a.page_size]) * a.page_size + tt % a.page_size;
-      }
-      kr[u] = ld128(kbase + slot * row_elems);
-      vr[u] = ld128(vbase + slot * row_elems);
+  for (int u = 0; u < U; ++u) {
+    const int t = min(beg + 4 * u + grp, end - 1);
+    off[u] = slot_offset<P1>(pages, t, a.page_size, row_elems);
+  }
+  for (int t0 = beg; t0 < end; t0 += kTile) {
+    uint4 kr[U], vr[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      kr[u] = ld128(kbase + off[u]);
+      vr[u] = ld128(vbase + off[u]);
+      ok[u] = t0 + 4 * u + grp < end;
     }
 #pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-      float s[kTokensPerLaneGroup];
-      float mx = m[gi];
-#pragma unroll
-      for (int u = 0; u < kTokensPerLaneGroup; ++u) {
-        s[u] = row16_sum(dot8<DT>(qv[gi], kr[u])) * a.scale_log2;
-        s[u] = valid[u] ? s[u] : -INFINITY;
-        mx = fmaxf(mx, s[u]);
-      }
-      const float corr = __builtin_amdgcn_exp2f(m[gi] - mx);
-      m[gi] = mx;
-      l[gi] *= corr;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[gi][i] *= corr;
-#pragma unroll
-      for (int u = 0; u < kTokensPerLaneGroup; ++u) {
-        const float p = __builtin_amdgcn_exp2f(s[u] - mx);
-        l[gi] += p;
-        float vf[8];
-        unpack8<DT>(vr[u], vf);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[gi][i] = fmaf(p, vf[i], o[gi][i]);
-      }
+    for (int u = 0; u < U; ++u) {  // next tile's slots, clamped into the chunk
+      const int t = min(t0 + kTile + 4 * u + grp, end - 1);
+      off[u] = slot_offset<P1>(pages, t, a.page_size, row_elems);
     }
+    consume<DT, G, U>(qv, kr, vr, ok, a.scale_log2, m, l, o);
   }
 
   // Combine the four 16-lane groups of the wave (each saw a token subset).
@@ -346,18 +448,20 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
     if (pslot < 0) {
       st128(a.out + req * a.out_stride_n + qh * a.out_stride_h + sub * 8, pack8<DT>(o[gi]));
     } else {
-      float* dst = a.partial_o + (static_cast<int64_t>(pslot) * a.num_q_heads + qh) * kHeadDim +
-                   sub * 8;
+      float* dst =
+          a.partial_o + (static_cast<int64_t>(pslot) * a.num_q_heads + qh) * kHeadDim + sub * 8;
       *reinterpret_cast<float4*>(dst) = make_float4(o[gi][0], o[gi][1], o[gi][2], o[gi][3]);
       *reinterpret_cast<float4*>(dst + 4) = make_float4(o[gi][4], o[gi][5], o[gi][6], o[gi][7]);
-      if (sub == 0)
+      if (sub == 0)  // log2-sum-exp of the chunk (v_log_f32 is log2)
         a.partial_lse[static_cast<int64_t>(pslot) * a.num_q_heads + qh] =
             m[gi] + __builtin_amdgcn_logf(l[gi]);
     }
   }
 }
 
-// Merge split-KV partials: one wave per (request, q head), two dims per lane.
+// Split-KV merge: one wave per (request, q head), two dims per lane. Chunks are
+// combined with a running log2-sum-exp; the chunk loop is unrolled so the
+// partial loads of several chunks are in flight together.
 template <int DT>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a, int32_t rows) {
   const int req = blockIdx.x;
@@ -367,32 +471,66 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a, int32_t rows) 
   const int first = a.ints[a.o_merge + 2 * req];
   const int count = a.ints[a.o_merge + 2 * req + 1];
   if (count <= 1) return;
-  float mx = -INFINITY;
-  for (int c = 0; c < count; ++c)
-    mx = fmaxf(mx, a.partial_lse[static_cast<int64_t>(first + c) * a.num_q_heads + qh]);
-  float acc0 = 0.f, acc1 = 0.f, den = 0.f;
-  for (int c = 0; c < count; ++c) {
-    const int64_t p = static_cast<int64_t>(first + c) * a.num_q_heads + qh;
-    const float wgt = __builtin_amdgcn_exp2f(a.partial_lse[p] - mx);
-    const float2 v = *reinterpret_cast<const float2*>(a.partial_o + p * kHeadDim + lane * 2);
-    acc0 = fmaf(wgt, v.x, acc0);
-    acc1 = fmaf(wgt, v.y, acc1);
-    den += wgt;
+  constexpr int kUnroll = 8;
+  float mx = -INFINITY, den = 0.f, acc0 = 0.f, acc1 = 0.f;
+  for (int c0 = 0; c0 < count; c0 += kUnroll) {
+    float lse[kUnroll];
+    float2 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int c = min(c0 + u, count - 1);
+      const int64_t p = static_cast<int64_t>(first + c) * a.num_q_heads + qh;
+      lse[u] = c0 + u < count ? a.partial_lse[p] : -INFINITY;
+      v[u] = *reinterpret_cast<const float2*>(a.partial_o + p * kHeadDim + lane * 2);
+    }
+    float m_new = mx;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) m_new = fmaxf(m_new, lse[u]);
+    const float corr = __builtin_amdgcn_exp2f(mx - m_new);
+    den *= corr;
+    acc0 *= corr;
+    acc1 *= corr;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const float wgt = __builtin_amdgcn_exp2f(lse[u] - m_new);
+      den += wgt;
+      acc0 = fmaf(wgt, v[u].x, acc0);
+      acc1 = fmaf(wgt, v[u].y, acc1);
+    }
+    mx = m_new;
   }
-  const uint32_t packed =
-      static_cast<uint32_t>(Elem<DT>::from_float(acc0 / den)) |
-      (static_cast<uint32_t>(Elem<DT>::from_float(acc1 / den)) << 16);
+  const uint32_t packed = static_cast<uint32_t>(Elem<DT>::from_float(acc0 / den)) |
+                          (static_cast<uint32_t>(Elem<DT>::from_float(acc1 / den)) << 16);
   *reinterpret_cast<uint32_t*>(a.out + req * a.out_stride_n + qh * a.out_stride_h + lane * 2) =
       packed;
+}
+
+// Tokens per 16-lane group per loop trip. Override with MI355X_DECODE_U
+// (2, 4 or 8; tuning knob, read once).
+int tokens_per_group() {
+  static const int value = [] {
+    const char* env = std::getenv("MI355X_DECODE_U");
+    const int v = env ? std::atoi(env) : 0;
+    return (v == 2 || v == 4 || v == 8) ? v : kTokensPerLaneGroup;
+  }();
+  return value;
 }
 
 template <int DT, int G>
 void launch_decode(const DecodeArgs& a, dim3 grid, int waves, bool p1, hipStream_t s) {
   const dim3 block(waves * kWave);
-  if (p1)
-    decode_kernel<DT, G, true><<<grid, block, 0, s>>>(a);
-  else
-    decode_kernel<DT, G, false><<<grid, block, 0, s>>>(a);
+  const int u = tokens_per_group();
+#define MI355X_DECODE_LAUNCH(P, UU) decode_kernel<DT, G, P, UU><<<grid, block, 0, s>>>(a)
+  if (p1) {
+    if (u == 2) MI355X_DECODE_LAUNCH(true, 2);
+    else if (u == 8) MI355X_DECODE_LAUNCH(true, 8);
+    else MI355X_DECODE_LAUNCH(true, 4);
+  } else {
+    if (u == 2) MI355X_DECODE_LAUNCH(false, 2);
+    else if (u == 8) MI355X_DECODE_LAUNCH(false, 8);
+    else MI355X_DECODE_LAUNCH(false, 4);
+  }
+#undef MI355X_DECODE_LAUNCH
 }
 
 template <int DT>
@@ -678,7 +816,7 @@ extern "C" const char* mi355x_decode_run(const void* plan_ptr, const void* q, in
   a.page_size = static_cast<int32_t>(page_size);
   a.scale_log2 = (1.0f / std::sqrt(static_cast<float>(kHeadDim))) * kLog2e;
 
-  const int waves = static_cast<int>(std::min<int64_t>(num_kv_heads, kMaxWavesPerBlock));
+  const int waves = static_cast<int>(waves_per_block(num_kv_heads));
   const int64_t grid_y = (num_kv_heads + waves - 1) / waves;
   // Graph plans launch the fixed capacity; surplus workgroups exit at once.
   const int64_t grid_x = p.graph ? p.items_capacity : p.num_items;
@@ -689,8 +827,7 @@ extern "C" const char* mi355x_decode_run(const void* plan_ptr, const void* q, in
                              : dispatch_group<1>(a, group, grid, waves, page_size == 1, s);
   if (!ok) return set_error("unsupported query group size");
   if (const char* err = launch_status("decode_kernel")) return err;
-  const bool any_split = p.graph || p.num_items > p.batch;
-  if (any_split) {
+  if (p.graph || p.num_items > p.batch) {  // some request was split
     const dim3 mgrid(static_cast<uint32_t>(batch), static_cast<uint32_t>((num_q_heads + 3) / 4));
     if (dtype == 0)
       merge_kernel<0><<<mgrid, dim3(256), 0, s>>>(a, static_cast<int32_t>(batch));
