@@ -41,6 +41,8 @@ def parse_args():
                    help="requests in the bounded CPU-baseline sample")
     p.add_argument("--decode-only", action="store_true",
                    help="skip the prefill and norm measurements")
+    p.add_argument("--only", choices=["prefill", "norms"],
+                   help="print only this section's measurements (tuning aid)")
     return p.parse_args()
 
 
@@ -232,6 +234,10 @@ def main():
     from llm_infer_rust_amd.kv_cache import BaseAttention
 
     dev = torch.device("cuda", 0)
+    if args.only:
+        fn = prefill_sections if args.only == "prefill" else norm_sections
+        print(json.dumps({args.only: fn(dev, max(args.steps, 20))}))
+        return
     w = build_workload(args.seed, dev)
     B, HQ, HKV, D = w["B"], w["HQ"], w["HKV"], w["D"]
     cache = BaseAttention()

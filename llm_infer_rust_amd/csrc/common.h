@@ -147,6 +147,14 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// s_waitcnt vmcnt(0): block until every outstanding vector-memory load of this
+// wave has returned. Used right after loading values that stay live across a
+// loop (e.g. the query rows), so the compiler's wait-count tracking does not
+// conservatively wait on the loop's own prefetch loads in every iteration.
+__device__ __forceinline__ void wait_vmem_loads() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt=0, expcnt=7, lgkmcnt=15 (gfx9 encoding)
+}
+
 // 128-bit global loads/stores.
 __device__ __forceinline__ uint4 ld128(const void* p) {
   return *reinterpret_cast<const uint4*>(p);

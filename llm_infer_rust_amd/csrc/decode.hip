@@ -384,8 +384,8 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
 #pragma unroll
   for (int gi = 0; gi < G; ++gi)
     qv[gi] = ld128(a.q + req * a.q_stride_n + (h * G + gi) * a.q_stride_h + sub * 8);
-
   const int32_t* pages = a.indices + a.ints[a.o_indptr + req];
+  wait_vmem_loads();
   const uint32_t row_elems = static_cast<uint32_t>(a.num_kv_heads) * kHeadDim;
   const uint16_t* kbase = a.k_cache + h * kHeadDim + sub * 8;
   const uint16_t* vbase = a.v_cache + h * kHeadDim + sub * 8;

@@ -93,20 +93,20 @@ __device__ __forceinline__ uint32_t hi16x2(uint32_t a, uint32_t b) {  // {a.hi, 
 
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return static_cast<uint32_t>(Elem<DT>::from_float(a)) |
-         (static_cast<uint32_t>(Elem<DT>::from_float(b)) << 16);
+  return Elem<DT>::pack2(a, b);
 }
 
 // HPB = q heads per workgroup (1, 2 or 4); BQ = 32 * 4 / HPB queries per workgroup.
 template <int DT, int HPB, bool PAGED>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds_k[2][kKStage];
   __shared__ __attribute__((aligned(16))) uint16_t lds_v[2][kVStage];
 
   constexpr int kWavesPerHead = kWaves / HPB;
   constexpr int kBQ = kQPerWave * kWavesPerHead;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  // Wave index as a scalar so every wave-level decision below is a uniform branch.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int col = lane & 31;   // query column / MFMA row index
   const int half = lane >> 5;  // k-half of the MFMA operands
@@ -132,32 +132,43 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     const uint16_t* qp = a.q + static_cast<int64_t>(rq.q_start + qi) * a.q_sn + qh * a.q_sh;
 #pragma unroll
     for (int s = 0; s < 8; ++s) qreg[s] = ld128(qp + 16 * s + 8 * half);
+    wait_vmem_loads();
   }
 
   // Global -> register staging of one K/V tile: 4 rows x 16 bytes per thread for each.
-  // K: row = tid/16 + 16 j, d chunk = tid%16. V: keys 4*(tid/16)+j, d chunk = tid%16.
+  // K: row = tid/16 + 16 j, d chunk = tid%16 (16 lanes read one 256-byte row).
+  // V: keys 4*(tid%16)+j, d chunk = tid/16, so the 16 lanes of an LDS phase write one
+  //    V^T row (16 x 8 contiguous bytes, no bank conflicts).
   const int ld_chunk = tid & 15;
   const int ld_row = tid >> 4;
-  uint4 kst[4], vst[4];
-  auto key_row = [&](int j, const uint16_t* base, int64_t sn, int64_t sh) -> const uint16_t* {
+  const int v_chunk = tid >> 4;
+  const int v_group = tid & 15;
+  uint4 ks0[4], vs0[4], ks1[4], vs1[4];  // two register stages: tiles t+1 and t+2
+  // Row pointers: ragged rows are q_start + j of the projection; paged rows are the
+  // cache slot of key j. One 32x32->64 multiply-add per row.
+  const uint32_t k_sn = static_cast<uint32_t>(a.k_sn), v_sn = static_cast<uint32_t>(a.v_sn);
+  const uint16_t* k_base = a.k + kvh * a.k_sh + ld_chunk * 8;
+  const uint16_t* v_base = a.v + kvh * a.v_sh + v_chunk * 8;
+  auto key_row = [&](int j, const uint16_t* base, uint32_t sn) -> const uint16_t* {
     j = min(j, kv_len - 1);
-    int64_t row;
+    uint32_t row;
     if constexpr (PAGED) {
-      row = static_cast<int64_t>(a.indices[rq.page_base + j / a.page_size]) * a.page_size +
-            j % a.page_size;
+      row = static_cast<uint32_t>(a.indices[rq.page_base + j / a.page_size]) *
+                static_cast<uint32_t>(a.page_size) +
+            static_cast<uint32_t>(j % a.page_size);
     } else {
-      row = rq.q_start + j;
+      row = static_cast<uint32_t>(rq.q_start + j);
     }
-    return base + row * sn + kvh * sh + ld_chunk * 8;
+    return base + static_cast<uint64_t>(row) * sn;
   };
-  auto load_tile = [&](int t) {
+  auto load_tile = [&](int t, uint4 (&kst)[4], uint4 (&vst)[4]) {
     const int k0 = t * kTileK;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) kst[j] = ld128(key_row(k0 + ld_row + 16 * j, a.k, a.k_sn, a.k_sh));
+    for (int j = 0; j < 4; ++j) kst[j] = ld128(key_row(k0 + ld_row + 16 * j, k_base, k_sn));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) vst[j] = ld128(key_row(k0 + 4 * ld_row + j, a.v, a.v_sn, a.v_sh));
+    for (int j = 0; j < 4; ++j) vst[j] = ld128(key_row(k0 + 4 * v_group + j, v_base, v_sn));
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int buf, const uint4 (&kst)[4], const uint4 (&vst)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       st128(&lds_k[buf][(ld_row + 16 * j) * kKPitch + ld_chunk * 8], kst[j]);
@@ -168,11 +179,11 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     const uint32_t w3[4] = {vst[3].x, vst[3].y, vst[3].z, vst[3].w};
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-      const int d = ld_chunk * 8 + 2 * p;
+      const int d = v_chunk * 8 + 2 * p;
       uint2 even = make_uint2(lo16x2(w0[p], w1[p]), lo16x2(w2[p], w3[p]));
       uint2 odd = make_uint2(hi16x2(w0[p], w1[p]), hi16x2(w2[p], w3[p]));
-      *reinterpret_cast<uint2*>(&lds_v[buf][d * kVPitch + 4 * ld_row]) = even;
-      *reinterpret_cast<uint2*>(&lds_v[buf][(d + 1) * kVPitch + 4 * ld_row]) = odd;
+      *reinterpret_cast<uint2*>(&lds_v[buf][d * kVPitch + 4 * v_group]) = even;
+      *reinterpret_cast<uint2*>(&lds_v[buf][(d + 1) * kVPitch + 4 * v_group]) = odd;
     }
   };
 
@@ -185,16 +196,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   const int my_q = wq0 + col;                // query (local index) of this lane
   const int my_horizon = rq.prefix + my_q;   // last visible key of this lane's query
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
-    const bool more = t + 1 < n_tiles;
-    if (more) load_tile(t + 1);
+  // Body for one 64-key tile held in LDS buffer `buf`.
+  auto compute = [&](int t, int buf) {
     const int k0 = t * kTileK;
     if (wave_active && k0 <= wave_last_key) {
       // S^T for 64 keys: two 32-key blocks.
@@ -208,24 +211,35 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
         for (int st = 0; st < 8; ++st)
           s[T] = Mfma<DT>::run(*reinterpret_cast<const uint4*>(krow + 16 * st), qreg[st], s[T]);
       }
-      const bool need_mask = k0 + kTileK - 1 > rq.prefix + wq0 || k0 + kTileK > kv_len;
+      // Only the diagonal / last tiles need the causal and length mask (uniform branch).
+      if (k0 + kTileK - 1 > rq.prefix + wq0 || k0 + kTileK > kv_len) {
+        const int limit = min(my_horizon, kv_len - 1) - (k0 + 4 * half);
+#pragma unroll
+        for (int T = 0; T < 2; ++T)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = 32 * T + (r >> 2) * 8 + (r & 3);
+            s[T][r] = key <= limit ? s[T][r] : -INFINITY;
+          }
+      }
       float mx = -INFINITY;
 #pragma unroll
       for (int T = 0; T < 2; ++T)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = s[T][r] * a.scale_log2;
-          if (need_mask) {
-            const int key = k0 + 32 * T + (r >> 2) * 8 + 4 * half + (r & 3);
-            x = (key <= my_horizon && key < kv_len) ? x : -INFINITY;
-          }
-          s[T][r] = x;
-          mx = fmaxf(mx, x);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-      m = m_new;
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[T][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;  // row max in log2 units
+      // Lazy rescale: the reference max m only moves when some row's max exceeds it
+      // by more than 8, so p = 2^(s - m) <= 2^8 and O/l are rescaled rarely.
+      if (__any(mx > m + 8.f)) {
+        const float m_new = fmaxf(m, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        m = m_new;
+        l *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      }
       float psum = 0.f;
       uint4 pb[4];  // P^T operands for the four 16-key k-steps
 #pragma unroll
@@ -235,17 +249,13 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
           float p[8];
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            p[i] = __builtin_amdgcn_exp2f(s[T][8 * hh + i] - m_new);
+            p[i] = __builtin_amdgcn_exp2f(fmaf(s[T][8 * hh + i], a.scale_log2, -m));
             psum += p[i];
           }
           pb[2 * T + hh] = make_uint4(pack2<DT>(p[0], p[1]), pack2<DT>(p[2], p[3]),
                                       pack2<DT>(p[4], p[5]), pack2<DT>(p[6], p[7]));
         }
-      l = l * alpha + psum;
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      l += psum;
       // O^T += V^T P^T. k-step st covers keys 16 st + {4 half + 0..3, 8 + 4 half + 0..3},
       // the same key order the S^T accumulators hold.
 #pragma unroll
@@ -259,7 +269,25 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
         }
       }
     }
-    if (more) store_tile(buf ^ 1);
+  };
+
+  // Two LDS buffers and two register stages: while tile t is consumed, tile t+1
+  // waits in registers (stored to LDS after the compute) and tile t+2 is in flight.
+  if (n_tiles > 0) {
+    load_tile(0, ks0, vs0);
+    store_tile(0, ks0, vs0);
+  }
+  if (n_tiles > 1) load_tile(1, ks1, vs1);
+  __syncthreads();
+  for (int t = 0; t < n_tiles; t += 2) {
+    if (t + 2 < n_tiles) load_tile(t + 2, ks0, vs0);
+    compute(t, 0);
+    if (t + 1 < n_tiles) store_tile(1, ks1, vs1);
+    __syncthreads();
+    if (t + 1 >= n_tiles) break;
+    if (t + 3 < n_tiles) load_tile(t + 3, ks1, vs1);
+    compute(t + 1, 1);
+    if (t + 2 < n_tiles) store_tile(0, ks0, vs0);
     __syncthreads();
   }
 
