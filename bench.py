@@ -27,6 +27,22 @@ import torch
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+COPY_CAL_BYTES = 256 << 20
+LAYERS = 4  # KV pools the decode steps rotate over (4 x 16 GiB)
+TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "decode_kernel_cfg2_traffic.txt")
+
+
+def measured_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary, if any."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        return None
+    return None
 METRIC = "decode-attn HBM GB/s (% peak); prefill MFMA util; output tok/s Qwen3-8B"
 
 
@@ -43,6 +59,9 @@ def parse_args():
                    help="skip the prefill and norm measurements")
     p.add_argument("--only", choices=["prefill", "norms"],
                    help="print only this section's measurements (tuning aid)")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="run one 256 MiB device-to-device copy first (PMC byte-count "
+                        "calibration for FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -59,17 +78,25 @@ def build_workload(seed: int, dev: torch.device):
         table[b, :n] = perm[off: off + n].to(torch.int32)
         off += n
     gd = torch.Generator(device=dev).manual_seed(seed)
-    kc = torch.randn(POOL, 1, HKV, D, generator=gd, device=dev, dtype=torch.bfloat16)
-    vc = torch.randn(POOL, 1, HKV, D, generator=gd, device=dev, dtype=torch.bfloat16)
-    kc[0].zero_()
-    vc[0].zero_()
+    # One KV pool per layer, as the model binds a separate [pages, P, Hkv, D] view per
+    # layer; steps rotate over them so no launch re-reads the previous launch's rows
+    # from the 256 MiB Infinity Cache.
+    kcs, vcs = [], []
+    for _ in range(LAYERS):
+        kc = torch.randn(POOL, 1, HKV, D, generator=gd, device=dev, dtype=torch.bfloat16)
+        vc = torch.randn(POOL, 1, HKV, D, generator=gd, device=dev, dtype=torch.bfloat16)
+        kc[0].zero_()
+        vc[0].zero_()
+        kcs.append(kc)
+        vcs.append(vc)
+    kc, vc = kcs[0], vcs[0]
     q = torch.randn(B, HQ, D, generator=gd, device=dev, dtype=torch.bfloat16)
     knew = torch.randn(B, HKV, D, generator=gd, device=dev, dtype=torch.bfloat16)
     vnew = torch.randn(B, HKV, D, generator=gd, device=dev, dtype=torch.bfloat16)
     loc = torch.tensor([int(table[b, int(lengths[b]) - 1]) for b in range(B)],
                        dtype=torch.int64, device=dev)
     return dict(B=B, HQ=HQ, HKV=HKV, D=D, POOL=POOL, lengths=lengths, table=table, kc=kc, vc=vc,
-                q=q, knew=knew, vnew=vnew, loc=loc)
+                kcs=kcs, vcs=vcs, q=q, knew=knew, vnew=vnew, loc=loc)
 
 
 def decode_bytes(lengths, hq, hkv, d) -> int:
@@ -203,19 +230,43 @@ def norm_sections(dev, reps: int) -> dict:
     from llm_infer_rust_amd import ops
 
     gd = torch.Generator(device=dev).manual_seed(33)
-    x = torch.randn(8192, 1024, generator=gd, device=dev, dtype=torch.bfloat16)
-    r = torch.randn(8192, 1024, generator=gd, device=dev, dtype=torch.bfloat16)
+    # Rotate over buffer sets (> 1 GiB in total) so reads come from HBM, not from the
+    # 256 MiB Infinity Cache left warm by the previous call.
+    sets = 24
+    xs = [torch.randn(8192, 1024, generator=gd, device=dev, dtype=torch.bfloat16)
+          for _ in range(sets)]
+    rs = [torch.randn(8192, 1024, generator=gd, device=dev, dtype=torch.bfloat16)
+          for _ in range(sets)]
+    outs = [torch.empty(8192, 1024, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
     w = torch.rand(1024, generator=gd, device=dev).add_(0.5).to(torch.bfloat16)
-    packed = torch.randn(8192, 4096, generator=gd, device=dev, dtype=torch.bfloat16)
-    q = packed[:, :2048].view(-1, 16, 128)
-    k = packed[:, 2048:3072].view(-1, 8, 128)
+    packs = [torch.randn(8192, 4096, generator=gd, device=dev, dtype=torch.bfloat16)
+             for _ in range(8)]
     qw = torch.rand(128, generator=gd, device=dev).add_(0.5).to(torch.bfloat16)
     kw = torch.rand(128, generator=gd, device=dev).add_(0.5).to(torch.bfloat16)
+    lib, stream = ops._native.lib(), torch.cuda.current_stream().cuda_stream
+    it = [0]
+
+    def rms():
+        i = it[0] = it[0] + 1
+        x, o = xs[i % sets], outs[i % sets]
+        ops._native.check(lib.mi355x_rms_norm(x.data_ptr(), w.data_ptr(), o.data_ptr(), 8192,
+                                              1, 1024, 1024, 0, 1e-6, 0, stream), "rms")
+
+    def add_rms():
+        i = it[0] = it[0] + 1
+        ops.add_rms_norm(xs[i % sets], rs[i % sets], w, 1e-6)
+
+    def qk():
+        i = it[0] = it[0] + 1
+        p = packs[i % len(packs)]
+        ops.qk_norm(p[:, :2048].view(-1, 16, 128), p[:, 2048:3072].view(-1, 8, 128), qw, kw,
+                    1e-6)
+
     res = {}
     for name, fn, nbytes in (
-            ("rms_norm", lambda: ops.rms_norm(x, w, 1e-6), 2 * 8192 * 1024 * 2),
-            ("add_rms_norm", lambda: ops.add_rms_norm(x, r, w, 1e-6), 4 * 8192 * 1024 * 2),
-            ("qk_norm", lambda: ops.qk_norm(q, k, qw, kw, 1e-6), 2 * 8192 * 24 * 128 * 2)):
+            ("rms_norm", rms, 2 * 8192 * 1024 * 2),
+            ("add_rms_norm", add_rms, 4 * 8192 * 1024 * 2),
+            ("qk_norm", qk, 2 * 8192 * 24 * 128 * 2)):
         ms = _event_time_ms(fn, reps)
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
@@ -238,11 +289,21 @@ def main():
         fn = prefill_sections if args.only == "prefill" else norm_sections
         print(json.dumps({args.only: fn(dev, max(args.steps, 20))}))
         return
+    if args.copy_calibration:
+        src = torch.empty(COPY_CAL_BYTES // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     w = build_workload(args.seed, dev)
     B, HQ, HKV, D = w["B"], w["HQ"], w["HKV"], w["D"]
-    cache = BaseAttention()
-    cache.set_reserved_write_slot(0)
-    cache.bind_kv_cache(w["kc"], w["vc"])
+    caches = []
+    for kc, vc in zip(w["kcs"], w["vcs"]):
+        c = BaseAttention()
+        c.set_reserved_write_slot(0)
+        c.bind_kv_cache(kc, vc)
+        caches.append(c)
     spec = AttentionSpec(HQ, HKV, D, torch.bfloat16, dev)
     table_d = w["table"].to(dev)
     lens_d = w["lengths"].to(dev)
@@ -255,16 +316,17 @@ def main():
     info = plan.info()
     out = torch.empty_like(w["q"])
 
-    def step():
-        cache.write_kv(w["knew"], w["vnew"], w["loc"])
-        run_decode(plan, w["q"], w["kc"], w["vc"], out)
+    def step(i):
+        c = caches[i % LAYERS]
+        c.write_kv(w["knew"], w["vnew"], w["loc"])
+        run_decode(plan, w["q"], c.k_cache, c.v_cache, out)
 
-    for _ in range(args.warmup):
-        step()
+    for i in range(args.warmup):
+        step(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
+    for i in range(args.steps):
+        step(i)
     torch.cuda.synchronize()
     step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
 
@@ -273,18 +335,19 @@ def main():
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(reps):
-        run_decode(plan, w["q"], w["kc"], w["vc"], out)
+    for i in range(reps):
+        run_decode(plan, w["q"], w["kcs"][i % LAYERS], w["vcs"][i % LAYERS], out)
     e1.record()
     torch.cuda.synchronize()
     decode_ms = e0.elapsed_time(e1) / reps
     e0.record()
-    for _ in range(reps):
-        cache.write_kv(w["knew"], w["vnew"], w["loc"])
+    for i in range(reps):
+        caches[i % LAYERS].write_kv(w["knew"], w["vnew"], w["loc"])
     e1.record()
     torch.cuda.synchronize()
     store_ms = e0.elapsed_time(e1) / reps
-    cache.check_write_errors()
+    for c in caches:
+        c.check_write_errors()
 
     dbytes = decode_bytes(w["lengths"], HQ, HKV, D)
     sbytes = store_bytes(B, HKV, D)
@@ -308,7 +371,7 @@ def main():
                    "split_kv_items": info["num_items"], "chunk_tokens": info["chunk_tokens"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": measured_traffic(),
                      "kernel": "decode_kernel+merge_kernel (one mi355x_decode_run)",
                      "algorithmic_bytes": dbytes, "avg_launch_us": round(decode_ms * 1e3, 3)},
         "kv_store": {"us": round(store_ms * 1e3, 3), "bytes": sbytes,
