@@ -16,7 +16,9 @@ from pathlib import Path
 
 import torch  # noqa: F401  (must precede loading the HIP library)
 
-LIB_PATH = Path(__file__).resolve().parent / "libmi355x_attn.so"
+# MI355X_ATTN_LIB overrides the library path (for comparing builds of the same sources).
+LIB_PATH = Path(os.environ.get("MI355X_ATTN_LIB",
+                               Path(__file__).resolve().parent / "libmi355x_attn.so"))
 
 c_void_p = ctypes.c_void_p
 c_i64 = ctypes.c_int64

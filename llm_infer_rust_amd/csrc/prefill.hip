@@ -22,6 +22,7 @@
 // a kv head are processed by the same workgroup so each K/V byte is fetched once per tile.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <memory>
@@ -34,13 +35,18 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kTileK = 64;             // keys per tile
-constexpr int kWaves = 4;              // waves per workgroup
 constexpr int kQPerWave = 32;          // queries per wave
 constexpr int kKPitch = kD + 8;        // LDS K row pitch (elements): conflict-free b128 reads
-constexpr int kVPitch = kTileK + 4;    // LDS V^T row pitch (elements): conflict-free b64 reads
+constexpr int kVPitch = kTileK + 8;    // LDS V^T row pitch (elements): conflict-free b128 reads
 constexpr int kKStage = kTileK * kKPitch;
 constexpr int kVStage = kD * kVPitch;
 constexpr float kLog2e = 1.4426950408889634f;
+
+// Ablation switches for performance decomposition builds (0 in the library):
+//   1: skip the softmax (P = constant), 2: skip the K/V global loads (tiles stay as is).
+#ifndef MI355X_PREFILL_ABLATE
+#define MI355X_PREFILL_ABLATE 0
+#endif
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -96,13 +102,29 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return Elem<DT>::pack2(a, b);
 }
 
-// HPB = q heads per workgroup (1, 2 or 4); BQ = 32 * 4 / HPB queries per workgroup.
-template <int DT, int HPB, bool PAGED>
-__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// c + a.lo * b.lo + a.hi * b.hi with fp32 accumulation (v_dot2_f32_bf16 / _f16).
+template <int DT>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (DT == 0) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+  } else {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b),
+                                  c, false);
+  }
+}
+
+// NW = waves per workgroup (4 or 8), HPB = q heads per workgroup; each head gets NW/HPB
+// waves of 32 queries, so BQ = 32 * NW / HPB queries per workgroup.
+template <int DT, int NW, int HPB, bool PAGED>
+__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds_k[2][kKStage];
   __shared__ __attribute__((aligned(16))) uint16_t lds_v[2][kVStage];
 
-  constexpr int kWavesPerHead = kWaves / HPB;
+  constexpr int kWavesPerHead = NW / HPB;
   constexpr int kBQ = kQPerWave * kWavesPerHead;
   const int tid = threadIdx.x;
   // Wave index as a scalar so every wave-level decision below is a uniform branch.
@@ -135,55 +157,94 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     wait_vmem_loads();
   }
 
-  // Global -> register staging of one K/V tile: 4 rows x 16 bytes per thread for each.
-  // K: row = tid/16 + 16 j, d chunk = tid%16 (16 lanes read one 256-byte row).
-  // V: keys 4*(tid%16)+j, d chunk = tid/16, so the 16 lanes of an LDS phase write one
-  //    V^T row (16 x 8 contiguous bytes, no bank conflicts).
-  const int ld_chunk = tid & 15;
-  const int ld_row = tid >> 4;
-  const int v_chunk = tid >> 4;
-  const int v_group = tid & 15;
-  uint4 ks0[4], vs0[4], ks1[4], vs1[4];  // two register stages: tiles t+1 and t+2
-  // Row pointers: ragged rows are q_start + j of the projection; paged rows are the
-  // cache slot of key j. One 32x32->64 multiply-add per row.
+  // Global -> register staging of a K/V tile (64 keys x 256 bytes each). A 256-thread
+  // slice stages K (row = st/16 + 16 j, 16-byte chunk st%16: 16 lanes read one row) and
+  // a 256-thread slice stages V (keys 4 (st%16) + j, chunk st/16: the 16 lanes of an LDS
+  // phase then write one contiguous V^T row). With 8 waves the two slices are different
+  // waves and share one register set; with 4 waves every thread stages both.
+  constexpr bool kSplit = NW == 8;
+  const int st = tid & 255;
+  const bool does_k = !kSplit || wave < 4;
+  const bool does_v = !kSplit || wave >= 4;
+  const int k_chunk = st & 15;
+  const int k_row = st >> 4;
+  const int v_chunk = st >> 4;
+  const int v_group = st & 15;
+  // Within each 16-key block a V^T row stores the key quads in the order
+  // {0-3, 8-11, 4-7, 12-15}: the 8 keys an MFMA lane needs for one k-step
+  // (16 st + 4 half + {0..3, 8..11}) are then one contiguous 16-byte read.
+  const int v_slot = (v_group & ~3) * 4 + ((v_group & 1) * 8 + (v_group & 2) * 2);
   const uint32_t k_sn = static_cast<uint32_t>(a.k_sn), v_sn = static_cast<uint32_t>(a.v_sn);
-  const uint16_t* k_base = a.k + kvh * a.k_sh + ld_chunk * 8;
-  const uint16_t* v_base = a.v + kvh * a.v_sh + v_chunk * 8;
-  auto key_row = [&](int j, const uint16_t* base, uint32_t sn) -> const uint16_t* {
-    j = min(j, kv_len - 1);
-    uint32_t row;
+  // Ragged rows are addressed from a workgroup-uniform base (the request's first row)
+  // with a 32-bit per-lane offset; paged rows from the slot index (64-bit product).
+  const uint16_t* k_req = a.k + kvh * a.k_sh + k_chunk * 8 +
+                          (PAGED ? 0 : static_cast<int64_t>(rq.q_start) * a.k_sn);
+  const uint16_t* v_req = a.v + kvh * a.v_sh + v_chunk * 8 +
+                          (PAGED ? 0 : static_cast<int64_t>(rq.q_start) * a.v_sn);
+  auto k_key = [&](int t, int j) { return t * kTileK + k_row + 16 * j; };
+  auto v_key = [&](int t, int j) { return t * kTileK + 4 * v_group + j; };
+
+  constexpr int kRows = kSplit ? 4 : 8;  // staged 16-byte rows per thread per tile
+  uint4 sa[kRows], sb[kRows];            // two register stages (tiles t+1 / t+2)
+  // Paged mode: page ids of a tile's rows are loaded one tile before the rows themselves
+  // (two alternating sets), so a row load never waits on its index load and the in-order
+  // vector-memory counter never has to drain earlier row loads.
+  int32_t pa[kRows], pb_[kRows];
+  auto load_pages = [&](int t, int32_t (&pg)[kRows]) {
     if constexpr (PAGED) {
-      row = static_cast<uint32_t>(a.indices[rq.page_base + j / a.page_size]) *
-                static_cast<uint32_t>(a.page_size) +
-            static_cast<uint32_t>(j % a.page_size);
-    } else {
-      row = static_cast<uint32_t>(rq.q_start + j);
+      int i = 0;
+      if (does_k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          pg[i++] = a.indices[rq.page_base + min(k_key(t, j), kv_len - 1) / a.page_size];
+      if (does_v)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          pg[(kSplit ? 0 : 4) + j] =
+              a.indices[rq.page_base + min(v_key(t, j), kv_len - 1) / a.page_size];
     }
-    return base + static_cast<uint64_t>(row) * sn;
   };
-  auto load_tile = [&](int t, uint4 (&kst)[4], uint4 (&vst)[4]) {
-    const int k0 = t * kTileK;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) kst[j] = ld128(key_row(k0 + ld_row + 16 * j, k_base, k_sn));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) vst[j] = ld128(key_row(k0 + 4 * v_group + j, v_base, v_sn));
+  auto row_ptr = [&](int j, int32_t page, const uint16_t* base, uint32_t sn) {
+    j = min(j, kv_len - 1);
+    if constexpr (PAGED) {
+      const uint32_t row = static_cast<uint32_t>(page) * static_cast<uint32_t>(a.page_size) +
+                           static_cast<uint32_t>(j % a.page_size);
+      return base + static_cast<uint64_t>(row) * sn;
+    } else {
+      return base + static_cast<uint32_t>(j) * sn;
+    }
   };
-  auto store_tile = [&](int buf, const uint4 (&kst)[4], const uint4 (&vst)[4]) {
+  auto load_tile = [&](int t, const int32_t (&pg)[kRows], uint4 (&sr)[kRows]) {
+    if (MI355X_PREFILL_ABLATE == 2 && t > 0) return;
+    if (does_k)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      st128(&lds_k[buf][(ld_row + 16 * j) * kKPitch + ld_chunk * 8], kst[j]);
-    // Transpose 4 keys x 8 dims into 8 rows of V^T (4 keys each, 8 bytes).
-    const uint32_t w0[4] = {vst[0].x, vst[0].y, vst[0].z, vst[0].w};
-    const uint32_t w1[4] = {vst[1].x, vst[1].y, vst[1].z, vst[1].w};
-    const uint32_t w2[4] = {vst[2].x, vst[2].y, vst[2].z, vst[2].w};
-    const uint32_t w3[4] = {vst[3].x, vst[3].y, vst[3].z, vst[3].w};
+      for (int j = 0; j < 4; ++j) sr[j] = ld128(row_ptr(k_key(t, j), pg[j], k_req, k_sn));
+    if (does_v)
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int d = v_chunk * 8 + 2 * p;
-      uint2 even = make_uint2(lo16x2(w0[p], w1[p]), lo16x2(w2[p], w3[p]));
-      uint2 odd = make_uint2(hi16x2(w0[p], w1[p]), hi16x2(w2[p], w3[p]));
-      *reinterpret_cast<uint2*>(&lds_v[buf][d * kVPitch + 4 * v_group]) = even;
-      *reinterpret_cast<uint2*>(&lds_v[buf][(d + 1) * kVPitch + 4 * v_group]) = odd;
+      for (int j = 0; j < 4; ++j)
+        sr[(kSplit ? 0 : 4) + j] =
+            ld128(row_ptr(v_key(t, j), pg[(kSplit ? 0 : 4) + j], v_req, v_sn));
+  };
+  auto store_tile = [&](int buf, const uint4 (&sr)[kRows]) {
+    if (does_k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        st128(&lds_k[buf][(k_row + 16 * j) * kKPitch + k_chunk * 8], sr[j]);
+    if (does_v) {
+      // Transpose 4 keys x 8 dims into 8 rows of V^T (4 keys each, 8 bytes).
+      const uint4* vs = sr + (kSplit ? 0 : 4);
+      const uint32_t w0[4] = {vs[0].x, vs[0].y, vs[0].z, vs[0].w};
+      const uint32_t w1[4] = {vs[1].x, vs[1].y, vs[1].z, vs[1].w};
+      const uint32_t w2[4] = {vs[2].x, vs[2].y, vs[2].z, vs[2].w};
+      const uint32_t w3[4] = {vs[3].x, vs[3].y, vs[3].z, vs[3].w};
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int d = v_chunk * 8 + 2 * p;
+        uint2 even = make_uint2(lo16x2(w0[p], w1[p]), lo16x2(w2[p], w3[p]));
+        uint2 odd = make_uint2(hi16x2(w0[p], w1[p]), hi16x2(w2[p], w3[p]));
+        *reinterpret_cast<uint2*>(&lds_v[buf][d * kVPitch + v_slot]) = even;
+        *reinterpret_cast<uint2*>(&lds_v[buf][(d + 1) * kVPitch + v_slot]) = odd;
+      }
     }
   };
 
@@ -208,8 +269,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
         for (int r = 0; r < 16; ++r) s[T][r] = 0.f;
         const uint16_t* krow = &lds_k[buf][(32 * T + col) * kKPitch + 8 * half];
 #pragma unroll
-        for (int st = 0; st < 8; ++st)
-          s[T] = Mfma<DT>::run(*reinterpret_cast<const uint4*>(krow + 16 * st), qreg[st], s[T]);
+        for (int kk = 0; kk < 8; ++kk)
+          s[T] = Mfma<DT>::run(*reinterpret_cast<const uint4*>(krow + 16 * kk), qreg[kk], s[T]);
       }
       // Only the diagonal / last tiles need the causal and length mask (uniform branch).
       if (k0 + kTileK - 1 > rq.prefix + wq0 || k0 + kTileK > kv_len) {
@@ -240,7 +301,6 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
       }
-      float psum = 0.f;
       uint4 pb[4];  // P^T operands for the four 16-key k-steps
 #pragma unroll
       for (int T = 0; T < 2; ++T)
@@ -248,52 +308,67 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
         for (int hh = 0; hh < 2; ++hh) {
           float p[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            p[i] = __builtin_amdgcn_exp2f(fmaf(s[T][8 * hh + i], a.scale_log2, -m));
-            psum += p[i];
-          }
+          for (int i = 0; i < 8; ++i)
+            p[i] = MI355X_PREFILL_ABLATE == 1
+                       ? s[T][8 * hh + i]
+                       : __builtin_amdgcn_exp2f(fmaf(s[T][8 * hh + i], a.scale_log2, -m));
           pb[2 * T + hh] = make_uint4(pack2<DT>(p[0], p[1]), pack2<DT>(p[2], p[3]),
                                       pack2<DT>(p[4], p[5]), pack2<DT>(p[6], p[7]));
         }
-      l += psum;
-      // O^T += V^T P^T. k-step st covers keys 16 st + {4 half + 0..3, 8 + 4 half + 0..3},
-      // the same key order the S^T accumulators hold.
+      // Row sum of the rounded P the PV product uses (v_dot2 against {1, 1}).
+      const uint32_t ones = pack2<DT>(1.f, 1.f);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        l = dot2<DT>(pb[kk].x, ones, l);
+        l = dot2<DT>(pb[kk].y, ones, l);
+        l = dot2<DT>(pb[kk].z, ones, l);
+        l = dot2<DT>(pb[kk].w, ones, l);
+      }
+      // O^T += V^T P^T; k-step kk covers keys 16 kk + 4 half + {0..3, 8..11}, the same
+      // order the S^T accumulators hold.
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const uint16_t* vrow = &lds_v[buf][(32 * db + col) * kVPitch + 4 * half];
+        const uint16_t* vrow = &lds_v[buf][(32 * db + col) * kVPitch + 8 * half];
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * st);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * st + 8);
-          o[db] = Mfma<DT>::run(make_uint4(lo.x, lo.y, hi.x, hi.y), pb[st], o[db]);
-        }
+        for (int kk = 0; kk < 4; ++kk)
+          o[db] = Mfma<DT>::run(*reinterpret_cast<const uint4*>(vrow + 16 * kk), pb[kk], o[db]);
       }
     }
   };
 
   // Two LDS buffers and two register stages: while tile t is consumed, tile t+1
   // waits in registers (stored to LDS after the compute) and tile t+2 is in flight.
+  // Page ids run one tile further ahead (pa: even tiles, pb_: odd tiles).
+  load_pages(0, pa);
+  load_pages(1, pb_);
   if (n_tiles > 0) {
-    load_tile(0, ks0, vs0);
-    store_tile(0, ks0, vs0);
+    load_tile(0, pa, sa);
+    store_tile(0, sa);
   }
-  if (n_tiles > 1) load_tile(1, ks1, vs1);
+  load_pages(2, pa);
+  if (n_tiles > 1) load_tile(1, pb_, sb);
+  load_pages(3, pb_);
   __syncthreads();
   for (int t = 0; t < n_tiles; t += 2) {
-    if (t + 2 < n_tiles) load_tile(t + 2, ks0, vs0);
+    if (t + 2 < n_tiles) {
+      load_tile(t + 2, pa, sa);
+      load_pages(t + 4, pa);
+    }
     compute(t, 0);
-    if (t + 1 < n_tiles) store_tile(1, ks1, vs1);
+    if (t + 1 < n_tiles) store_tile(1, sb);
     __syncthreads();
     if (t + 1 >= n_tiles) break;
-    if (t + 3 < n_tiles) load_tile(t + 3, ks1, vs1);
+    if (t + 3 < n_tiles) {
+      load_tile(t + 3, pb_, sb);
+      load_pages(t + 5, pb_);
+    }
     compute(t + 1, 1);
-    if (t + 2 < n_tiles) store_tile(0, ks0, vs0);
+    if (t + 2 < n_tiles) store_tile(0, sa);
     __syncthreads();
   }
 
   if (!wave_active || my_q >= rq.q_len) return;
-  const float lt = l + __shfl_xor(l, 32);
-  const float inv = 1.f / lt;
+  const float inv = 1.f / (l + __shfl_xor(l, 32));
   uint16_t* op = a.out + static_cast<int64_t>(rq.q_start + my_q) * a.o_sn + qh * a.o_sh;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -347,7 +422,23 @@ struct Buffer {
   ~Buffer() { release(); }
 };
 
-int heads_per_block(int64_t group) { return group >= 4 ? 4 : static_cast<int>(group); }
+// Waves per prefill workgroup: 8 (one workgroup per CU, 2 waves per SIMD, twice the
+// queries per K/V tile) for paged plans, whose long cached prefixes make K/V staging
+// the cost to amortise; 4 (two workgroups per CU, more workgroups) for ragged plans,
+// whose causal tail favours finer work items. Measured on MI355X at configs 3 and 4.
+// MI355X_PREFILL_WAVES=4|8 overrides both (tuning knob, read once).
+int prefill_waves(bool paged) {
+  static const int forced = [] {
+    const char* env = std::getenv("MI355X_PREFILL_WAVES");
+    const int v = env ? std::atoi(env) : 0;
+    return (v == 4 || v == 8) ? v : 0;
+  }();
+  return forced ? forced : (paged ? 8 : 4);
+}
+
+int heads_per_block(int64_t group, int waves) {
+  return static_cast<int>(std::min<int64_t>(group, waves));
+}
 
 }  // namespace
 
@@ -356,6 +447,7 @@ struct PrefillPlan {
   int64_t num_q_heads = 0, num_kv_heads = 0, page_size = 0, dtype = 0;
   int64_t batch = 0, total_q = 0, num_items = 0, total_pages = 0;
   bool paged = false;
+  int waves = 8;  // waves per workgroup the work list was built for
   // Device int32 workspace: [req info 4*B][work 4*items][kv_indptr B+1][last_len B]
   int64_t o_work = 0, o_indptr = 0, o_last = 0;
   Buffer ints, indices, staging;
@@ -383,9 +475,12 @@ extern "C" int64_t mi355x_prefill_schedule(const int32_t* q_host, const int32_t*
       num_q_heads % num_kv_heads != 0)
     return -1;
   const int64_t group = num_q_heads / num_kv_heads;
-  const int hpb = heads_per_block(group);
+  bool paged = false;
+  for (int64_t r = 0; r < batch; ++r) paged |= prefix_host[r] > 0;
+  const int waves = prefill_waves(paged);
+  const int hpb = heads_per_block(group, waves);
   if (group % hpb) return -1;
-  const int bq = kQPerWave * (kWaves / hpb);
+  const int bq = kQPerWave * (waves / hpb);
   struct Item {
     int64_t cost;
     int32_t r, q0, kvh, hg;
@@ -555,6 +650,7 @@ extern "C" void* mi355x_prefill_prepare(void* existing, const int32_t* q_indptr,
     plan->num_items = n_items;
     plan->total_pages = total_pages;
     plan->paged = paged;
+    plan->waves = prefill_waves(paged);
     plan->o_work = o_work;
     plan->o_indptr = o_indptr;
     plan->o_last = o_last;
@@ -608,22 +704,26 @@ extern "C" const char* mi355x_prefill_plan_read(const void* plan, int32_t* kv_in
 
 namespace mi355x {
 namespace {
-template <int DT, int HPB>
+template <int DT, int NW, int HPB>
 void launch_prefill(const PrefillArgs& a, bool paged, hipStream_t s) {
-  const dim3 grid(static_cast<uint32_t>(a.num_items)), block(256);
+  const dim3 grid(static_cast<uint32_t>(a.num_items)), block(64 * NW);
   if (paged)
-    prefill_kernel<DT, HPB, true><<<grid, block, 0, s>>>(a);
+    prefill_kernel<DT, NW, HPB, true><<<grid, block, 0, s>>>(a);
   else
-    prefill_kernel<DT, HPB, false><<<grid, block, 0, s>>>(a);
+    prefill_kernel<DT, NW, HPB, false><<<grid, block, 0, s>>>(a);
 }
 template <int DT>
-void launch_dt(const PrefillArgs& a, int hpb, bool paged, hipStream_t s) {
-  if (hpb == 1)
-    launch_prefill<DT, 1>(a, paged, s);
-  else if (hpb == 2)
-    launch_prefill<DT, 2>(a, paged, s);
-  else
-    launch_prefill<DT, 4>(a, paged, s);
+void launch_dt(const PrefillArgs& a, int waves, int hpb, bool paged, hipStream_t s) {
+  if (waves == 8) {
+    if (hpb == 1) launch_prefill<DT, 8, 1>(a, paged, s);
+    else if (hpb == 2) launch_prefill<DT, 8, 2>(a, paged, s);
+    else if (hpb == 4) launch_prefill<DT, 8, 4>(a, paged, s);
+    else launch_prefill<DT, 8, 8>(a, paged, s);
+  } else {
+    if (hpb == 1) launch_prefill<DT, 4, 1>(a, paged, s);
+    else if (hpb == 2) launch_prefill<DT, 4, 2>(a, paged, s);
+    else launch_prefill<DT, 4, 4>(a, paged, s);
+  }
 }
 }  // namespace
 }  // namespace mi355x
@@ -666,11 +766,12 @@ extern "C" const char* mi355x_prefill_run(const void* plan_ptr, const void* q, i
   a.num_kv_heads = static_cast<int32_t>(num_kv_heads);
   a.page_size = static_cast<int32_t>(p.paged ? page_size : 1);
   a.scale_log2 = (1.0f / std::sqrt(static_cast<float>(kD))) * kLog2e;
-  const int hpb = heads_per_block(num_q_heads / num_kv_heads);
+  const int waves = p.waves;
+  const int hpb = heads_per_block(num_q_heads / num_kv_heads, waves);
   auto s = static_cast<hipStream_t>(stream);
   if (dtype == 0)
-    launch_dt<0>(a, hpb, p.paged, s);
+    launch_dt<0>(a, waves, hpb, p.paged, s);
   else
-    launch_dt<1>(a, hpb, p.paged, s);
+    launch_dt<1>(a, waves, hpb, p.paged, s);
   return launch_status("prefill_kernel");
 }
