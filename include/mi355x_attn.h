@@ -196,6 +196,65 @@ int64_t mi355x_prefill_schedule(const int32_t* q_host, const int32_t* prefix_hos
                                 int64_t num_q_heads, int64_t num_kv_heads, int32_t* work,
                                 int64_t capacity);
 
+/* ------------------------------------------------------------------------
+ * Decoder-layer elementwise ops (dtype 0 = bf16, 1 = fp16).
+ * ------------------------------------------------------------------------ */
+
+/* Half-split rotary embedding of every q and k head, in place:
+ *   x[i] <- x[i] cos - x[i+W/2] sin,  x[i+W/2] <- x[i+W/2] cos + x[i] sin,
+ * cos/sin fp32 [max_positions, W/2], positions int64 [tokens]; a position
+ * outside [0, max_positions) leaves its token untouched.
+ * Replaces sglang_layers_native_rope (src/layers/fused_ops.cu:340-346). */
+const char* mi355x_rope(void* q, void* k, const int64_t* positions, const float* cos,
+                        const float* sin, int64_t tokens, int64_t q_heads, int64_t k_heads,
+                        int64_t width, int64_t q_token_stride, int64_t q_head_stride,
+                        int64_t k_token_stride, int64_t k_head_stride, int64_t max_positions,
+                        int dtype, void* stream);
+
+/* One pass of the decoder layer's qk_norm -> rope -> K/V store
+ * (src/models/qwen3/model.rs:478-514; base.rs:62-152), width 128 only.
+ * Each stage is optional: q_weight/k_weight NULL skips the norm, positions
+ * NULL skips the rotation, k_cache NULL skips the store. q and k are updated
+ * in place; the stored K row is the rotated one and V is copied unchanged.
+ * Results equal mi355x_qk_norm, mi355x_rope and mi355x_store_kv run in turn
+ * (the normalised value is rounded before it is rotated). Store semantics
+ * (reserved slot, out-of-range slot, error_count) are those of
+ * mi355x_store_kv with heads = k_heads. No single reference counterpart: it
+ * fuses sglang_layers_native_qk_norm, _rope and sglang_native_store_kv. */
+const char* mi355x_qk_norm_rope_store(
+    void* q, void* k, const void* v, const void* q_weight, const void* k_weight,
+    const int64_t* positions, const float* cos, const float* sin, int64_t max_positions,
+    void* k_cache, void* v_cache, const void* loc, bool index64, int64_t capacity,
+    int64_t reserved, int32_t* error_count, int64_t tokens, int64_t q_heads, int64_t k_heads,
+    int64_t width, int64_t q_token_stride, int64_t q_head_stride, int64_t k_token_stride,
+    int64_t k_head_stride, int64_t v_token_stride, int64_t v_head_stride, double eps, int dtype,
+    void* stream);
+
+/* out[t, c] = silu(gate_up[t, c]) * gate_up[t, W + c]; gate_up [tokens, 2W]
+ * and out [tokens, W] contiguous.
+ * Replaces sglang_layers_native_silu_mul (src/layers/fused_ops.cu:364-366). */
+const char* mi355x_silu_mul(const void* gate_up, void* out, int64_t tokens, int64_t width,
+                            int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Sampling.
+ * ------------------------------------------------------------------------ */
+
+/* One token id per logits row (dtype 0 = bf16, 1 = fp16, 2 = fp32; row
+ * stride in elements). temperature/top_k/top_p are per-row device arrays,
+ * normalised as SamplingParams::normalized: temperature <= 0 or top_p == 0
+ * gives the argmax; otherwise joint top-k/top-p filtering on the original
+ * softmax(logits / temperature) and one draw from the survivors. An invalid
+ * distribution (NaN, or no finite logit) gives -1. The draw is a function of
+ * (seed, offset, row, logits) only: equal arguments give equal tokens.
+ * Replaces sglang_sampling_native (src/engine/sampling_flashinfer.cu:4-6)
+ * plus the temperature/softmax/argmax steps of Sampler::sample
+ * (src/engine/sampling.rs:239-269), for a whole heterogeneous batch at once. */
+const char* mi355x_sample(const void* logits, int64_t rows, int64_t vocab, int64_t row_stride,
+                          int dtype, const float* temperature, const int32_t* top_k,
+                          const float* top_p, uint64_t seed, uint64_t offset, int64_t* out,
+                          void* stream);
+
 #pragma GCC visibility pop
 
 #ifdef __cplusplus

@@ -70,6 +70,16 @@ SIGNATURES: dict[str, tuple] = {
     "mi355x_prefill_plan_read": (c_char_p, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "mi355x_prefill_schedule": (c_i64, [c_void_p, c_void_p, c_i64, c_i64, c_i64, c_void_p,
                                         c_i64]),
+    "mi355x_rope": (c_char_p, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_i64, c_i64,
+                               c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_int, c_void_p]),
+    "mi355x_qk_norm_rope_store": (c_char_p, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                             c_void_p, c_void_p, c_void_p, c_i64, c_void_p,
+                                             c_void_p, c_void_p, c_bool, c_i64, c_i64, c_void_p,
+                                             c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                             c_i64, c_i64, c_i64, c_double, c_int, c_void_p]),
+    "mi355x_silu_mul": (c_char_p, [c_void_p, c_void_p, c_i64, c_i64, c_int, c_void_p]),
+    "mi355x_sample": (c_char_p, [c_void_p, c_i64, c_i64, c_i64, c_int, c_void_p, c_void_p,
+                                 c_void_p, c_u64, c_u64, c_void_p, c_void_p]),
 }
 
 _lock = threading.Lock()

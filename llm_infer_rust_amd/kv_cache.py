@@ -117,6 +117,10 @@ class BaseAttention:
             v.stride(0), v.stride(1), self._reserved_write_slot,
             write_loc.dtype == torch.int64, self._errors.data_ptr(), stream_of(k)), "KV store")
 
+    def error_word(self) -> torch.Tensor | None:
+        """Device int32 counter of rejected (out-of-range) slots."""
+        return self._errors
+
     def check_write_errors(self) -> None:
         """Raise if any earlier write_kv saw a slot outside the cache (synchronises)."""
         if self._errors is None:

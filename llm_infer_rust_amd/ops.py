@@ -9,9 +9,18 @@ validation of its ATen bridge ``src/layers/fused_ops_bridge.cpp:56-118``:
 * ``qk_norm(q, k, q_weight, k_weight, eps)`` normalises q and k views of a
   packed QKV buffer in place and returns ``(q, k)``; V is never written.
 
+and ``src/layers/ops.rs:53-127``:
+
+* ``silu_and_mul(gate_up)`` returns a new ``[T, W]`` tensor;
+* ``HalfSplitRope`` holds fp32 cos/sin tables and rotates q/k in place;
+* ``qk_norm_rope_store`` runs the decoder layer's qk_norm -> rope -> K/V store
+  as one pass (``src/models/qwen3/model.rs:478-514``).
+
 Only CUDA(HIP) bfloat16/float16 tensors are accepted; anything else raises.
 """
 from __future__ import annotations
+
+import math
 
 import torch
 
@@ -78,4 +87,130 @@ def qk_norm(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor, k_weight: 
     return q, k
 
 
-__all__ = ["rms_norm", "add_rms_norm", "qk_norm", "NativeError", "_native"]
+def silu_and_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(gate) * up for a packed ``[T, 2W]`` input (ops.rs:53-61)."""
+    _require_device(gate_up, "silu_and_mul")
+    dt = dtype_code(gate_up)
+    if gate_up.dim() != 2 or gate_up.size(1) % 2 != 0 or not gate_up.is_contiguous():
+        raise NativeError("invalid SiLU input: expected a contiguous [T, 2W] tensor")
+    width = gate_up.size(1) // 2
+    if out is None:
+        out = torch.empty((gate_up.size(0), width), dtype=gate_up.dtype, device=gate_up.device)
+    elif (out.shape != (gate_up.size(0), width) or out.dtype != gate_up.dtype
+          or not out.is_contiguous() or out.device != gate_up.device):
+        raise NativeError("invalid SiLU output")
+    check(lib().mi355x_silu_mul(gate_up.data_ptr(), out.data_ptr(), gate_up.size(0), width, dt,
+                                stream_of(gate_up)), "silu_and_mul")
+    return out
+
+
+class HalfSplitRope:
+    """Shared rotary tables (ops.rs:65-97): fp32 cos/sin ``[max_positions, D/2]`` on the GPU."""
+
+    def __init__(self, max_positions: int, head_dim: int, rope_theta: float,
+                 device: torch.device | str):
+        if head_dim % 2 != 0 or max_positions <= 0:
+            raise NativeError("invalid RoPE geometry")
+        inv_freq = torch.exp(torch.arange(0, head_dim, 2, dtype=torch.float32)
+                             * (-(math.log(rope_theta) / head_dim)))
+        positions = torch.arange(max_positions, dtype=torch.float32)
+        freqs = positions.unsqueeze(-1) * inv_freq.unsqueeze(0)
+        self.cos = freqs.cos().to(device)
+        self.sin = freqs.sin().to(device)
+        self.half_dim = head_dim // 2
+        self.max_positions = max_positions
+
+    def apply(self, q: torch.Tensor, k: torch.Tensor,
+              positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Rotate q [T, Hq, D] and k [T, Hkv, D] views in place; returns (q, k)."""
+        return rope(q, k, positions, self.cos, self.sin)
+
+
+def _check_heads(q: torch.Tensor, k: torch.Tensor, what: str) -> None:
+    if (q.dim() != 3 or k.dim() != 3 or q.size(0) != k.size(0) or q.size(2) != k.size(2)
+            or q.device != k.device or q.dtype != k.dtype or q.stride(2) != 1
+            or k.stride(2) != 1):
+        raise NativeError(f"invalid {what} query/key shapes or strides")
+
+
+def _check_positions(q: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
+                     sin: torch.Tensor) -> None:
+    if (positions.dtype != torch.int64 or positions.dim() != 1 or positions.numel() != q.size(0)
+            or not positions.is_contiguous() or positions.device != q.device):
+        raise NativeError("RoPE positions must be a contiguous int64 vector, one per token")
+    half = q.size(2) // 2
+    for table in (cos, sin):
+        if (table.dtype != torch.float32 or table.dim() != 2 or table.size(1) != half
+                or not table.is_contiguous() or table.device != q.device):
+            raise NativeError("RoPE tables must be contiguous fp32 [max_positions, D/2]")
+
+
+def rope(q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
+         sin: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """In-place half-split RoPE (fused_ops.cu:108-133 semantics)."""
+    _require_device(q, "rope")
+    dt = dtype_code(q)
+    _check_heads(q, k, "RoPE")
+    _check_positions(q, positions, cos, sin)
+    check(lib().mi355x_rope(q.data_ptr(), k.data_ptr(), positions.data_ptr(), cos.data_ptr(),
+                            sin.data_ptr(), q.size(0), q.size(1), k.size(1), q.size(2),
+                            q.stride(0), q.stride(1), k.stride(0), k.stride(1), cos.size(0), dt,
+                            stream_of(q)), "rope")
+    return q, k
+
+
+def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       q_weight: torch.Tensor | None, k_weight: torch.Tensor | None, eps: float,
+                       positions: torch.Tensor | None, rope_tables: HalfSplitRope | None,
+                       attention=None, write_loc: torch.Tensor | None = None) -> None:
+    """qk_norm -> rope -> K/V store in one pass; q and k are rewritten in place.
+
+    ``attention`` is a bound ``kv_cache.BaseAttention`` (its caches, reserved slot and error
+    word are used); the store is skipped when it is None or ``write_loc`` is None, as
+    ``BaseAttention.write_kv`` skips it."""
+    _require_device(q, "qk_norm_rope_store")
+    dt = dtype_code(q)
+    _check_heads(q, k, "QK-norm/RoPE")
+    if v.shape != k.shape or v.stride(2) != 1 or v.dtype != k.dtype:
+        raise NativeError("K/V input must have matching (tokens, kv_heads, head_dim) shapes")
+    if (q_weight is None) != (k_weight is None):
+        raise NativeError("q_weight and k_weight go together")
+    if q_weight is not None:
+        _check_weight(q, q_weight, q.size(2))
+        _check_weight(k, k_weight, k.size(2))
+    cos = sin = None
+    max_pos = 0
+    if rope_tables is not None:
+        if positions is None:
+            raise NativeError("RoPE needs positions")
+        cos, sin, max_pos = rope_tables.cos, rope_tables.sin, rope_tables.max_positions
+        _check_positions(q, positions, cos, sin)
+    kc = vc = errors = None
+    reserved, capacity, index64 = -1, 0, False
+    if attention is not None and write_loc is not None and attention.is_bound():
+        kc, vc = attention.cache_tensors()
+        if kc.size(2) != k.size(1) or kc.size(3) != k.size(2) or kc.dtype != k.dtype:
+            raise NativeError("K/V input head shape does not match the bound cache")
+        if (write_loc.dim() != 1 or write_loc.numel() != k.size(0) or not write_loc.is_contiguous()
+                or write_loc.dtype not in (torch.int32, torch.int64)
+                or write_loc.device != k.device):
+            raise NativeError("invalid KV store locations")
+        reserved = attention.reserved_write_slot()
+        capacity = kc.size(0) * kc.size(1)
+        index64 = write_loc.dtype == torch.int64
+        errors = attention.error_word()
+
+    def ptr(t):
+        return None if t is None else t.data_ptr()
+
+    check(lib().mi355x_qk_norm_rope_store(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), ptr(q_weight), ptr(k_weight),
+        ptr(positions) if rope_tables is not None else None, ptr(cos), ptr(sin), max_pos,
+        ptr(kc), ptr(vc), ptr(write_loc) if kc is not None else None, index64, capacity,
+        reserved, ptr(errors), q.size(0), q.size(1), k.size(1), q.size(2), q.stride(0),
+        q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1), float(eps), dt,
+        stream_of(q)), "qk_norm_rope_store")
+
+
+__all__ = ["rms_norm", "add_rms_norm", "qk_norm", "silu_and_mul", "HalfSplitRope", "rope",
+           "qk_norm_rope_store", "NativeError", "_native"]
