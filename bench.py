@@ -43,6 +43,61 @@ def measured_traffic():
     except OSError:
         return None
     return None
+def e2e_section(dev, args) -> dict:
+    """Qwen3-8B shapes, random bf16 weights N(0, 0.02) (seeded), 256
+    requests x 1024 random ids -> 512 output tokens each, continuous batching, hipGraph decode,
+    joint sampling T 0.7 / top-k 50 / top-p 0.9 with a fixed seed. All requests arrive at t=0;
+    TTFT is arrival -> first sampled token on the host."""
+    from llm_infer_rust_amd.engine import Engine, EngineConfig
+    from llm_infer_rust_amd.model import Qwen3Config, Qwen3Model
+    from llm_infer_rust_amd.sampling import SamplingParams
+    import dataclasses
+    import numpy as np
+
+    cfg = Qwen3Config.qwen3_8b()
+    if args.e2e_layers:
+        cfg = dataclasses.replace(cfg, num_layers=args.e2e_layers)
+    t0 = time.perf_counter()
+    model = Qwen3Model(cfg, torch.bfloat16, dev).init_random(seed=args.seed)
+    n_req, n_in, n_out = args.e2e_requests, args.e2e_input, args.e2e_output
+    eng = Engine(model, EngineConfig(page_size=16, max_running_req=256,
+                                     max_prefill_tokens_per_batch=8192,
+                                     max_seq_len=n_in + n_out, seed=args.seed))
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t0
+    rng = np.random.default_rng(args.seed)
+    params = SamplingParams(temperature=0.7, top_k=50, top_p=0.9, ignore_eos=True,
+                            max_tokens=n_out)
+    prompts = [rng.integers(0, cfg.vocab_size, n_in) for _ in range(n_req)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    reqs = [eng.add_request(p, params) for p in prompts]
+    eng.run_until_complete()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ttft = sorted((r.first_token_time - r.arrival) * 1e3 for r in reqs)
+    out_tokens = sum(len(r.output) for r in reqs)
+    result = {
+        "output_tok_s": round(out_tokens / wall, 1),
+        "p50_ttft_ms": round(statistics.median(ttft), 1),
+        "p90_ttft_ms": round(ttft[int(0.9 * (len(ttft) - 1))], 1),
+        "wall_s": round(wall, 3),
+        "output_tokens": out_tokens,
+        "input_tokens": n_req * n_in,
+        "prefill_batches": eng.stats["prefill_batches"],
+        "decode_steps": eng.stats["decode_steps"],
+        "graph_steps": eng.stats["graph_steps"],
+        "setup_s": round(setup_s, 1),
+        "config": {"model": "Qwen3-8B shape (random bf16 N(0,0.02) weights)",
+                   "layers": cfg.num_layers, "requests": n_req, "input": n_in,
+                   "output": n_out, "page_size": 16, "max_prefill_tokens": 8192,
+                   "sampling": "T0.7 k50 p0.9 seed %d" % args.seed},
+    }
+    del eng, model
+    torch.cuda.empty_cache()
+    return result
+
+
 METRIC = "decode-attn HBM GB/s (% peak); prefill MFMA util; output tok/s Qwen3-8B"
 
 
@@ -59,6 +114,12 @@ def parse_args():
                    help="skip the prefill and norm measurements")
     p.add_argument("--only", choices=["prefill", "norms"],
                    help="print only this section's measurements (tuning aid)")
+    p.add_argument("--e2e-requests", type=int, default=256)
+    p.add_argument("--e2e-input", type=int, default=1024)
+    p.add_argument("--e2e-output", type=int, default=512)
+    p.add_argument("--e2e-layers", type=int, default=None,
+                   help="override the layer count (smoke runs only; the reported config is 36)")
+    p.add_argument("--skip-e2e", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
                    help="run one 256 MiB device-to-device copy first (PMC byte-count "
                         "calibration for FETCH_SIZE / WRITE_SIZE)")
@@ -349,6 +410,7 @@ def main():
     for c in caches:
         c.check_write_errors()
 
+    cpu = cpu_baseline(w, args.cpu_requests) if not args.no_cpu_baseline else None
     dbytes = decode_bytes(w["lengths"], HQ, HKV, D)
     sbytes = store_bytes(B, HKV, D)
     achieved = dbytes / (decode_ms * 1e-3) / 1e9
@@ -378,11 +440,16 @@ def main():
                      "GB/s": round(sbytes / (store_ms * 1e-3) / 1e9, 2)},
         "plan_prepare_ms": round(plan_ms, 3),
     }
+    if cpu is not None:
+        result["cpu_baseline"] = cpu
     if not args.decode_only:
         result["prefill"] = prefill_sections(dev, reps)
         result["norms"] = norm_sections(dev, reps)
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(w, args.cpu_requests)
+    # The decode workload's 64 GiB of KV pools are released before the e2e model is built.
+    del w, caches, plan, out, table_d, lens_d, meta, step, c
+    torch.cuda.empty_cache()
+    if not args.skip_e2e and not args.decode_only:
+        result["e2e"] = e2e_section(dev, args)
     print(json.dumps(result))
 
 

@@ -84,6 +84,10 @@ class AttentionMetadata:
     req_to_token: torch.Tensor | None = None
     cache_seqlens: torch.Tensor | None = None
     max_seqlen: int | None = None
+    # Scheduler-side host copies of cu_seqlens_q / prefix_lens. When present the backend
+    # plans from them instead of reading the device tensors back (no sync per forward).
+    host_cu_seqlens_q: list[int] | None = None
+    host_prefix_lens: list[int] | None = None
 
 
 @dataclass
@@ -102,9 +106,12 @@ class PrefillMetadata:
     def prepare(metadata: AttentionMetadata | None, total_tokens: int) -> "PrefillMetadata":
         boundaries = batch_boundaries(metadata, total_tokens)
         if metadata is not None and metadata.forward_mode == BatchPhase.PREFILL:
-            if metadata.prefix_lens is None:
+            if metadata.host_prefix_lens is not None:
+                prefixes = [int(x) for x in metadata.host_prefix_lens]
+            elif metadata.prefix_lens is None:
                 raise ModelError("missing prefix_lens")
-            prefixes = [int(x) for x in metadata.prefix_lens.cpu().tolist()]
+            else:
+                prefixes = [int(x) for x in metadata.prefix_lens.cpu().tolist()]
         else:
             prefixes = [0] * (len(boundaries) - 1)
         if len(prefixes) + 1 != len(boundaries) or any(p < 0 for p in prefixes):
@@ -117,15 +124,18 @@ class PrefillMetadata:
 
 def batch_boundaries(metadata: AttentionMetadata | None, total_tokens: int) -> list[int]:
     if metadata is None or metadata.forward_mode == BatchPhase.DECODE \
-            or metadata.cu_seqlens_q is None:
+            or (metadata.cu_seqlens_q is None and metadata.host_cu_seqlens_q is None):
         return [0, total_tokens]
     return prefill_boundaries(metadata, total_tokens)
 
 
 def prefill_boundaries(metadata: AttentionMetadata, total_tokens: int) -> list[int]:
-    if metadata.cu_seqlens_q is None:
+    if metadata.host_cu_seqlens_q is not None:
+        b = [int(x) for x in metadata.host_cu_seqlens_q]
+    elif metadata.cu_seqlens_q is None:
         raise ModelError("cached prefill requires cu_seqlens_q")
-    b = [int(x) for x in metadata.cu_seqlens_q.cpu().tolist()]
+    else:
+        b = [int(x) for x in metadata.cu_seqlens_q.cpu().tolist()]
     if (len(b) < 2 or b[0] != 0 or b[-1] != total_tokens
             or any(b[i] >= b[i + 1] for i in range(len(b) - 1))):
         raise ModelError("invalid prefill cu_seqlens_q")

@@ -1,0 +1,401 @@
+"""Continuous-batching serving loop around the Qwen3 model on the gfx950 path.
+
+Mirrors the parts of the reference engine that feed the attention hot path:
+
+* ``EngineConfig`` defaults from ``ServerArgs`` (``src/engine/engine.rs:64-82``): page size 16,
+  256 running requests, 8192 prefill tokens per batch, decode graphs for batch sizes
+  1, 2, 4, ..., 256;
+* the serial scheduler step (``src/scheduler/scheduler.rs:205-271``): one prefill batch (FIFO,
+  token budget, the last request chunked when it does not fit), then one decode step over every
+  running request;
+* batch metadata (``src/engine/batch_context.rs:216-360``, ``src/scheduler/decode.rs:168-422``):
+  int32 ``block_table`` / ``cache_seqlens`` / ``cu_seqlens_q`` / ``prefix_lens``, slots
+  ``page * page_size + offset`` for ``write_loc``. The host keeps the block table, lengths and
+  positions incrementally (a request's row changes only when it gains a page) and uploads one
+  pinned staging block per step; the planner reads host lengths, never device ones;
+* ``DecodeGraphRunner`` (``src/engine/graph.rs:26-329``): fixed input buffers per captured batch
+  size, pad rows pointing at the reserved page 0 (length 1, slot 0 skipped by the K/V store),
+  and the attention plan re-made outside the graph before each replay
+  (``DecodeGraphState.prepare_replay``);
+* sampling with a pinned asynchronous readback (``src/engine/sampling.rs:193-237``).
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from .backend import AttentionMetadata, BatchPhase, DecodeHostMetadata
+from .kv_cache import KVCacheLayout, KVCachePool, ModelError
+from .model import Qwen3Model
+from .sampling import Sampler, SamplingParams
+
+
+@dataclass
+class EngineConfig:
+    page_size: int = 16
+    max_running_req: int = 256
+    max_prefill_tokens_per_batch: int = 8192
+    max_seq_len: int = 4096
+    num_pages: int | None = None           # default: every running request at max_seq_len
+    graph_batch_sizes: tuple[int, ...] | None = None  # default 1, 2, 4, ... <= max_running_req
+    use_graphs: bool = True
+    seed: int = 0
+
+
+@dataclass(eq=False)
+class Request:
+    uid: int
+    prompt: np.ndarray
+    params: SamplingParams
+    eos_token_id: int | None = None
+    output: list[int] = field(default_factory=list)
+    pages: list[int] = field(default_factory=list)
+    cursor: int = 0                 # prompt tokens already in the cache
+    admitted: bool = False          # holds a running slot
+    arrival: float = 0.0
+    first_token_time: float | None = None
+    finish_time: float | None = None
+
+    @property
+    def cached_len(self) -> int:
+        """Tokens whose K/V are in the cache (the prompt cursor, then every fed output)."""
+        return self.cursor + max(len(self.output) - 1, 0)
+
+    def finished(self) -> bool:
+        if not self.output:
+            return False
+        if len(self.output) >= self.params.max_tokens:
+            return True
+        return (not self.params.ignore_eos and self.eos_token_id is not None
+                and self.output[-1] == self.eos_token_id)
+
+
+class PageAllocator:
+    """Physical pages 1..num_pages; page 0 is the reserved zero page."""
+
+    def __init__(self, num_pages: int):
+        self.free = list(range(num_pages, 0, -1))
+
+    def alloc(self, n: int) -> list[int]:
+        if n > len(self.free):
+            raise ModelError("out of KV-cache pages")
+        out = self.free[-n:][::-1] if n else []
+        del self.free[len(self.free) - n:]
+        return out
+
+    def release(self, pages: list[int]) -> None:
+        self.free.extend(reversed(pages))
+
+
+def _words(a: np.ndarray) -> np.ndarray:
+    """An int32/int64 array as a flat run of 8-byte words (int32 padded to an even count)."""
+    flat = np.ascontiguousarray(a).reshape(-1)
+    if flat.dtype == np.int32:
+        if flat.size % 2:
+            flat = np.concatenate([flat, np.zeros(1, np.int32)])
+        return flat.view(np.int64)
+    return flat.astype(np.int64, copy=False)
+
+
+def _views(block: torch.Tensor, arrays) -> list[torch.Tensor]:
+    """Typed views of a word block laid out as ``_words`` packs ``arrays``."""
+    out, off = [], 0
+    for a in arrays:
+        if a.dtype == np.int32:
+            words = (a.size + 1) // 2
+            out.append(block[off:off + words].view(torch.int32)[:a.size].view(a.shape))
+        else:
+            words = a.size
+            out.append(block[off:off + words].view(a.shape))
+        off += words
+    return out
+
+
+class _DecodeGraph:
+    """One captured decode step; its inputs are views of one device word block."""
+
+    def __init__(self, bs: int, cols: int, vocab: int, device: torch.device,
+                 dtype: torch.dtype):
+        self.bs = bs
+        shapes = (np.zeros(bs, np.int64), np.zeros(bs, np.int64), np.zeros(bs, np.int64),
+                  np.zeros(bs, np.int32), np.zeros((bs, cols), np.int32))
+        words = sum(_words(a).size for a in shapes)
+        self.block = torch.zeros(words, dtype=torch.int64, device=device)
+        (self.input_ids, self.positions, self.write_loc, self.cache_seqlens,
+         self.block_table) = _views(self.block, shapes)
+        self.cache_seqlens.fill_(1)
+        self.logits = torch.empty(bs, vocab, dtype=dtype, device=device)
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self.state = None
+        self.batch = None
+
+
+class Engine:
+    def __init__(self, model: Qwen3Model, config: EngineConfig | None = None):
+        self.model = model
+        self.cfg = config or EngineConfig()
+        cfg, mcfg = self.cfg, model.cfg
+        self.device = model.device
+        self.page_size = cfg.page_size
+        self.cols = -(-cfg.max_seq_len // cfg.page_size)
+        num_pages = cfg.num_pages or cfg.max_running_req * self.cols
+        self.pool = KVCachePool(KVCacheLayout(mcfg.num_layers, num_pages, cfg.page_size,
+                                              mcfg.num_kv_heads, mcfg.head_dim),
+                                model.dtype, self.device)
+        model.bind_kv_cache(self.pool, reserved_slot=0)
+        self.pages = PageAllocator(num_pages)
+        self.sampler = Sampler(cfg.seed)
+        self.waiting: list[Request] = []
+        self.running: list[Request] = []
+        self.finished: list[Request] = []
+        self._next_uid = 0
+        # Host mirror of the decode block table, one row per running request (by uid).
+        self._rows: dict[int, np.ndarray] = {}
+        self._staging = torch.empty(0, dtype=torch.int64, pin_memory=True)
+        self.graphs: dict[int, _DecodeGraph] = {}
+        self.stats = {"prefill_batches": 0, "decode_steps": 0, "graph_steps": 0}
+        if cfg.use_graphs:
+            self.capture_graphs()
+
+    # ------------------------------------------------------------------ requests
+    def add_request(self, prompt, params: SamplingParams,
+                    eos_token_id: int | None = None) -> Request:
+        prompt = np.asarray(prompt, dtype=np.int64)
+        params = params.normalized()
+        if prompt.ndim != 1 or prompt.size == 0:
+            raise ModelError("prompt must be a non-empty 1-D id list")
+        if prompt.size + params.max_tokens > self.cfg.max_seq_len:
+            raise ModelError("prompt + max_tokens exceeds max_seq_len")
+        req = Request(self._next_uid, prompt, params, eos_token_id, arrival=time.perf_counter())
+        self._next_uid += 1
+        self.waiting.append(req)
+        return req
+
+    def _ensure_pages(self, req: Request, tokens: int) -> None:
+        need = -(-tokens // self.page_size) - len(req.pages)
+        if need > 0:
+            new = self.pages.alloc(need)
+            start = len(req.pages)
+            req.pages.extend(new)
+            row = self._rows.setdefault(req.uid, np.zeros(self.cols, np.int32))
+            row[start:start + need] = new
+
+    def _slots(self, req: Request, start: int, stop: int) -> np.ndarray:
+        pos = np.arange(start, stop)
+        pages = np.asarray(req.pages, np.int64)
+        return pages[pos // self.page_size] * self.page_size + pos % self.page_size
+
+    def _pack(self, arrays) -> int:
+        """Copy int32/int64 arrays into the pinned staging buffer as 8-byte words."""
+        words = [_words(a) for a in arrays]
+        total = sum(w.size for w in words)
+        if self._staging.numel() < total:
+            self._staging = torch.empty(max(total, 2 * self._staging.numel()), dtype=torch.int64,
+                                        pin_memory=True)
+        host = self._staging.numpy()
+        off = 0
+        for w in words:
+            host[off:off + w.size] = w
+            off += w.size
+        return total
+
+    def _upload(self, *arrays: np.ndarray) -> list[torch.Tensor]:
+        """One pinned staging block, one host-to-device copy; returns typed device views."""
+        total = self._pack(arrays)
+        dev = self._staging[:total].to(self.device, non_blocking=True)
+        return _views(dev, arrays)
+
+    # ------------------------------------------------------------------ prefill
+    def _select_prefill(self) -> list[tuple[Request, int]]:
+        budget = self.cfg.max_prefill_tokens_per_batch
+        picked: list[tuple[Request, int]] = []
+        admitted = len(self.running)
+        # A chunked request continues first (scheduler/prefill.rs select_continuation).
+        queue = [r for r in self.running if r.cursor < r.prompt.size] + self.waiting
+        for req in queue:
+            if budget <= 0:
+                break
+            if not req.admitted:
+                if admitted >= self.cfg.max_running_req:
+                    break
+                admitted += 1
+            remaining = req.prompt.size - req.cursor
+            take = min(remaining, budget)
+            if take < remaining:  # chunks end on a page boundary
+                take -= (req.cursor + take) % self.page_size
+                if take <= 0:
+                    break
+            picked.append((req, take))
+            budget -= take
+        return picked
+
+    def _run_prefill(self, picked: list[tuple[Request, int]]) -> None:
+        ids, pos, loc, cu, prefixes, table = [], [], [], [0], [], []
+        last_rows = []
+        for req, take in picked:
+            if not req.admitted:
+                req.admitted = True
+                self.waiting.remove(req)
+                self.running.append(req)
+            start = req.cursor
+            self._ensure_pages(req, start + take)
+            ids.append(req.prompt[start:start + take])
+            pos.append(np.arange(start, start + take))
+            loc.append(self._slots(req, start, start + take))
+            prefixes.append(start)
+            cu.append(cu[-1] + take)
+            table.append(self._rows[req.uid])
+            if start + take == req.prompt.size:
+                last_rows.append(cu[-1] - 1)
+        n = cu[-1]
+        ids_d, pos_d, loc_d, idx_d, cu_d, prefix_d, table_d = self._upload(
+            np.concatenate(ids), np.concatenate(pos), np.concatenate(loc),
+            np.asarray(last_rows, np.int64), np.asarray(cu, np.int32),
+            np.asarray(prefixes, np.int32), np.stack(table).astype(np.int32))
+        meta = AttentionMetadata(BatchPhase.PREFILL, write_loc=loc_d, cu_seqlens_q=cu_d,
+                                 prefix_lens=prefix_d, block_table=table_d,
+                                 host_cu_seqlens_q=cu, host_prefix_lens=prefixes)
+        batch = self.model.attention.prepare(meta, n)
+        # Logits only for requests whose prompt ends in this batch (possibly none).
+        logits = self.model.forward(ids_d, pos_d, batch, loc_d, idx_d)
+        del batch
+        for req, take in picked:
+            req.cursor += take
+        done = [req for req, _ in picked if req.cursor == req.prompt.size]
+        self.stats["prefill_batches"] += 1
+        if done:
+            self._sample_and_commit(logits, done)
+
+    # ------------------------------------------------------------------ decode
+    def _decode_rows(self) -> list[Request]:
+        return [r for r in self.running if r.cursor == r.prompt.size and r.output
+                and not r.finished()]
+
+    def _run_decode(self, rows: list[Request]) -> None:
+        n = len(rows)
+        pos = np.empty(n, np.int64)
+        ids = np.empty(n, np.int64)
+        for i, req in enumerate(rows):
+            p = req.cached_len          # position of the token being fed
+            self._ensure_pages(req, p + 1)
+            pos[i] = p
+            ids[i] = req.output[-1]
+        pages = np.asarray([req.pages[p // self.page_size] for req, p in zip(rows, pos)],
+                           np.int64)
+        loc = pages * self.page_size + pos % self.page_size
+        lens = (pos + 1).astype(np.int32)
+        graph = self._graph_for(n)
+        if graph is not None:
+            self._replay(graph, rows, ids, pos, loc, lens)
+            logits = graph.logits[:n]
+            self.stats["graph_steps"] += 1
+        else:
+            table = np.stack([self._rows[r.uid] for r in rows])
+            ids_d, pos_d, loc_d, lens_d, table_d = self._upload(ids, pos, loc, lens, table)
+            meta = AttentionMetadata(BatchPhase.DECODE, decode_host=DecodeHostMetadata(
+                lens.tolist()), write_loc=loc_d, block_table=table_d, cache_seqlens=lens_d)
+            batch = self.model.attention.prepare(meta, n)
+            logits = self.model.forward(ids_d, pos_d, batch, loc_d)
+            del batch
+        self.stats["decode_steps"] += 1
+        self._sample_and_commit(logits, rows)
+
+    def _sample_and_commit(self, logits: torch.Tensor, rows: list[Request]) -> None:
+        pending = self.sampler.defer_batch(logits, [r.params for r in rows])
+        ids = pending.finish()
+        now = time.perf_counter()
+        for req, tok in zip(rows, ids):
+            req.output.append(int(tok))
+            if req.first_token_time is None:
+                req.first_token_time = now
+            if req.finished():
+                req.finish_time = now
+        for req in [r for r in rows if r.finished()]:
+            self.running.remove(req)
+            self.finished.append(req)
+            self.pages.release(req.pages)
+            req.pages = []
+            self._rows.pop(req.uid, None)
+
+    # ------------------------------------------------------------------ graphs
+    def _bucket_sizes(self) -> list[int]:
+        if self.cfg.graph_batch_sizes is not None:
+            return sorted(set(self.cfg.graph_batch_sizes))
+        out, bs = [], 1
+        while bs < self.cfg.max_running_req:
+            out.append(bs)
+            bs *= 2
+        out.append(self.cfg.max_running_req)
+        return sorted(set(out))
+
+    def _graph_for(self, n: int) -> _DecodeGraph | None:
+        for bs in sorted(self.graphs):
+            if bs >= n:
+                return self.graphs[bs]
+        return None
+
+    def capture_graphs(self) -> None:
+        """Capture one decode step per bucket, largest first, sharing one memory pool."""
+        model = self.model
+        pool = torch.cuda.graph_pool_handle()
+        for bs in sorted(self._bucket_sizes(), reverse=True):
+            g = _DecodeGraph(bs, self.cols, model.cfg.vocab_size, self.device, model.dtype)
+            meta = AttentionMetadata(BatchPhase.DECODE, write_loc=g.write_loc,
+                                     block_table=g.block_table, cache_seqlens=g.cache_seqlens)
+            g.state = model.attention.prepare_decode_graph(meta)
+            g.state.prepare_replay(DecodeHostMetadata([1] * bs))
+            g.batch = model.attention.prepare(meta, bs)
+            side = torch.cuda.Stream(self.device)
+            side.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(side):  # warm-up run: library workspaces, hipBLASLt choice
+                model.forward(g.input_ids, g.positions, g.batch, g.write_loc,
+                              logits_out=g.logits)
+            torch.cuda.current_stream(self.device).wait_stream(side)
+            torch.cuda.synchronize(self.device)
+            g.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g.graph, pool=pool):
+                model.forward(g.input_ids, g.positions, g.batch, g.write_loc,
+                              logits_out=g.logits)
+            torch.cuda.synchronize(self.device)
+            self.graphs[bs] = g
+
+    def _replay(self, g: _DecodeGraph, rows: list[Request], ids: np.ndarray, pos: np.ndarray,
+                loc: np.ndarray, lens: np.ndarray) -> None:
+        n, bs = len(rows), g.bs
+        pad = bs - n
+        table = np.zeros((bs, self.cols), np.int32)  # pad rows: page 0
+        for i, req in enumerate(rows):
+            table[i] = self._rows[req.uid]
+        # Pad rows: token 0 at position 0, slot 0 (the reserved slot), length 1.
+        arrays = (np.concatenate([ids, np.zeros(pad, np.int64)]),
+                  np.concatenate([pos, np.zeros(pad, np.int64)]),
+                  np.concatenate([loc, np.zeros(pad, np.int64)]),
+                  np.concatenate([lens, np.ones(pad, np.int32)]), table)
+        total = self._pack(arrays)
+        g.block.copy_(self._staging[:total], non_blocking=True)  # one copy into the graph inputs
+        g.state.prepare_replay(DecodeHostMetadata(lens.tolist()))
+        g.graph.replay()
+
+    # ------------------------------------------------------------------ loop
+    def step(self) -> None:
+        picked = self._select_prefill()
+        if picked:
+            self._run_prefill(picked)
+        rows = self._decode_rows()
+        if rows:
+            self._run_decode(rows)
+
+    def has_work(self) -> bool:
+        return bool(self.waiting or self.running)
+
+    def run_until_complete(self) -> list[Request]:
+        while self.has_work():
+            self.step()
+        self.model.check_write_errors()
+        return self.finished
+
+
+__all__ = ["Engine", "EngineConfig", "Request", "PageAllocator"]
