@@ -112,7 +112,7 @@ def parse_args():
                    help="requests in the bounded CPU-baseline sample")
     p.add_argument("--decode-only", action="store_true",
                    help="skip the prefill and norm measurements")
-    p.add_argument("--only", choices=["prefill", "norms"],
+    p.add_argument("--only", choices=["prefill", "norms", "e2e"],
                    help="print only this section's measurements (tuning aid)")
     p.add_argument("--e2e-requests", type=int, default=256)
     p.add_argument("--e2e-input", type=int, default=1024)
@@ -323,11 +323,23 @@ def norm_sections(dev, reps: int) -> dict:
         ops.qk_norm(p[:, :2048].view(-1, 16, 128), p[:, 2048:3072].view(-1, 8, 128), qw, kw,
                     1e-6)
 
+    # Decode-size residual norm of the Qwen3-8B e2e step: 256 rows x 4096.
+    dx = [torch.randn(256, 4096, generator=gd, device=dev, dtype=torch.bfloat16)
+          for _ in range(sets)]
+    dr = [torch.randn(256, 4096, generator=gd, device=dev, dtype=torch.bfloat16)
+          for _ in range(sets)]
+    w4 = torch.rand(4096, generator=gd, device=dev).add_(0.5).to(torch.bfloat16)
+
+    def add_rms_decode():
+        i = it[0] = it[0] + 1
+        ops.add_rms_norm(dx[i % sets], dr[i % sets], w4, 1e-6)
+
     res = {}
     for name, fn, nbytes in (
             ("rms_norm", rms, 2 * 8192 * 1024 * 2),
             ("add_rms_norm", add_rms, 4 * 8192 * 1024 * 2),
-            ("qk_norm", qk, 2 * 8192 * 24 * 128 * 2)):
+            ("qk_norm", qk, 2 * 8192 * 24 * 128 * 2),
+            ("add_rms_norm_256x4096", add_rms_decode, 4 * 256 * 4096 * 2)):
         ms = _event_time_ms(fn, reps)
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
@@ -346,6 +358,9 @@ def main():
     from llm_infer_rust_amd.kv_cache import BaseAttention
 
     dev = torch.device("cuda", 0)
+    if args.only == "e2e":
+        print(json.dumps({"e2e": e2e_section(dev, args)}))
+        return
     if args.only:
         fn = prefill_sections if args.only == "prefill" else norm_sections
         print(json.dumps({args.only: fn(dev, max(args.steps, 20))}))

@@ -94,7 +94,13 @@ __global__ __launch_bounds__(256) void norm_vec(NormArgs a) {
   const int chunks = static_cast<int>(a.width >> 3);
 
   float vals[NCH][8];
+  uint4 wraw[NCH];  // weights issued with the row, off the reduction's critical path
   float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int chunk = lane + c * LPR;
+    if (chunk < chunks) wraw[c] = ld128(w + chunk * 8);
+  }
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int chunk = lane + c * LPR;
@@ -118,7 +124,61 @@ __global__ __launch_bounds__(256) void norm_vec(NormArgs a) {
     const int chunk = lane + c * LPR;
     if (chunk < chunks) {
       float wf[8];
-      unpack8<DT>(ld128(w + chunk * 8), wf);
+      unpack8<DT>(wraw[c], wf);
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = (vals[c][i] * scale) * wf[i];
+      st128(dst + chunk * 8, pack8<DT>(y));
+    }
+  }
+}
+
+// Few wide rows (decode-size batches of hidden rows): one 256-lane workgroup per
+// row so a batch of a few hundred rows still spreads over every CU. Each lane
+// holds NCH 128-bit chunks; the sum of squares crosses waves through LDS.
+template <int DT, int MODE, int NCH>
+__global__ __launch_bounds__(256) void norm_row_block(NormArgs a) {
+  __shared__ float partial[4];
+  const int64_t row = blockIdx.x;
+  uint16_t *src, *dst, *res;
+  const uint16_t* w;
+  row_pointers<MODE>(a, row, src, dst, res, w);
+  const int chunks = static_cast<int>(a.width >> 3);
+  float vals[NCH][8];
+  uint4 wraw[NCH];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int chunk = threadIdx.x + c * 256;
+    if (chunk < chunks) wraw[c] = ld128(w + chunk * 8);
+  }
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int chunk = threadIdx.x + c * 256;
+    if (chunk < chunks) {
+      unpack8<DT>(ld128(src + chunk * 8), vals[c]);
+      if constexpr (MODE == kAddRms) {
+        float r[8];
+        unpack8<DT>(ld128(res + chunk * 8), r);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vals[c][i] += r[i];
+        st128(res + chunk * 8, pack8<DT>(vals[c]));
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(vals[c][i], vals[c][i], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if (threadIdx.x % kWave == 0) partial[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  ss = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+  const float scale = rsqrtf(ss / static_cast<float>(a.width) + a.eps);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int chunk = threadIdx.x + c * 256;
+    if (chunk < chunks) {
+      float wf[8];
+      unpack8<DT>(wraw[c], wf);
       float y[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) y[i] = (vals[c][i] * scale) * wf[i];
@@ -167,6 +227,17 @@ const char* dispatch(const NormArgs& a, bool vec, hipStream_t s, const char* nam
   if (vec && chunks <= 32) {
     const int64_t blocks = (a.rows + 15) / 16;
     norm_vec<DT, MODE, 16, 2><<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, s>>>(a);
+    return launch_status(name);
+  }
+  // Wide rows, too few of them to give every CU four rows: a workgroup per row.
+  if (vec && chunks > 128 && chunks <= 256 * 4 && a.rows < 4 * 256 * 4) {
+    const dim3 grid(static_cast<uint32_t>(a.rows));
+    if (chunks <= 256)
+      norm_row_block<DT, MODE, 1><<<grid, dim3(256), 0, s>>>(a);
+    else if (chunks <= 512)
+      norm_row_block<DT, MODE, 2><<<grid, dim3(256), 0, s>>>(a);
+    else
+      norm_row_block<DT, MODE, 4><<<grid, dim3(256), 0, s>>>(a);
     return launch_status(name);
   }
   if (vec && chunks <= 64 * 8) {

@@ -36,7 +36,8 @@ def check(actual, expected_f32, dtype, tol):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("rows,width", [(3, 1024), (1, 8), (65, 4096), (7, 13), (2, 16384)])
+@pytest.mark.parametrize("rows,width", [(3, 1024), (1, 8), (65, 4096), (7, 13), (2, 16384),
+                                        (256, 4096), (300, 2056), (4100, 4096)])
 def test_rms_norm(gpu, dtype, rows, width):
     g = torch.Generator().manual_seed(rows * width)
     x = torch.randn(rows, width, generator=g).to(dtype).to(gpu)
@@ -57,7 +58,7 @@ def test_rms_norm_row_stride(gpu):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("tokens", [1, 3, 65])
-@pytest.mark.parametrize("width", [13, 1024])
+@pytest.mark.parametrize("width", [13, 1024, 4096])
 def test_add_rms_norm_matches_fp32_sum(gpu, dtype, tokens, width):
     g = torch.Generator().manual_seed(19 + tokens + width)
     x = torch.randn(tokens, width, generator=g).to(dtype).to(gpu)
