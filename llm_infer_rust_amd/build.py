@@ -34,6 +34,8 @@ COMMON_FLAGS = [
     f"-I{INCLUDE}",
     # Keep the compiler from forming packed fp32 ops (v_pk_*_f32).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # The direct-to-LDS copies set m0 in inline asm (declared clobbered).
+    "-Wno-inline-asm",
 ]
 
 

@@ -11,15 +11,16 @@
 // Mode rule (flashinfer_bridge.cpp:266-273): paged iff some prefix > 0; ragged mode reads
 // K/V straight from the (packed) projection rows, paged mode from the KV cache pages.
 //
-// Kernel design. One workgroup = 4 waves = one (request, query tile, kv head, head group).
-// Each wave owns 32 queries of one q head and keeps, per 64-key tile:
+// Kernel design. One workgroup = 8 waves (two per SIMD) = one (request, query tile, kv
+// head, head group). Each wave owns 32 queries of one q head and keeps, per 64-key tile:
 //   S^T = K Q^T      (v_mfma_f32_32x32x16: A = K rows from LDS, B = Q^T from registers)
-//   O^T += V^T P^T   (A = V^T rows from a transposed LDS copy, B = P^T straight from the
-//                     S^T accumulators, no LDS round trip)
+//   O^T += V^T P^T   (A = V^T read transposed from the row-major V tile with
+//                     ds_read_b64_tr_b16, B = P^T straight from the S^T accumulators)
 // In this transposed form each lane holds one query column, so the online-softmax max/sum
 // and the O rescale are per-lane register work plus one cross-half exchange per tile.
-// K/V tiles are double-buffered in LDS (one barrier per tile); the g q heads that share
-// a kv head are processed by the same workgroup so each K/V byte is fetched once per tile.
+// K/V tiles stream through a 4-deep LDS ring filled by direct global -> LDS copies (one
+// barrier per tile); the g q heads that share a kv head are processed by the same
+// workgroup so each K/V byte is fetched once per tile.
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -34,19 +35,14 @@ namespace mi355x {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kTileK = 64;             // keys per tile
-constexpr int kQPerWave = 32;          // queries per wave
-constexpr int kKPitch = kD + 8;        // LDS K row pitch (elements): conflict-free b128 reads
-constexpr int kVPitch = kTileK + 8;    // LDS V^T row pitch (elements): conflict-free b128 reads
-constexpr int kKStage = kTileK * kKPitch;
-constexpr int kVStage = kD * kVPitch;
+constexpr int kTileK = 64;                    // keys per tile
+constexpr int kQPerWave = 32;                 // queries per wave
+constexpr int kWaves = 8;                     // waves per workgroup
+constexpr int kStages = 4;                    // LDS ring depth (tiles)
+constexpr int kTileBytes = kTileK * kD * 2;   // 16 KB per K or V tile
+constexpr int kStageBytes = 2 * kTileBytes;   // K + V
 constexpr float kLog2e = 1.4426950408889634f;
-
-// Ablation switches for performance decomposition builds (0 in the library):
-//   1: skip the softmax (P = constant), 2: skip the K/V global loads (tiles stay as is).
-#ifndef MI355X_PREFILL_ABLATE
-#define MI355X_PREFILL_ABLATE 0
-#endif
+constexpr int kMaxKvLen = 1 << 22;            // div_small is exact below this
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -90,13 +86,6 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-__device__ __forceinline__ uint32_t lo16x2(uint32_t a, uint32_t b) {  // {a.lo, b.lo}
-  return __builtin_amdgcn_perm(b, a, 0x05040100u);
-}
-__device__ __forceinline__ uint32_t hi16x2(uint32_t a, uint32_t b) {  // {a.hi, b.hi}
-  return __builtin_amdgcn_perm(b, a, 0x07060302u);
-}
-
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return Elem<DT>::pack2(a, b);
@@ -117,37 +106,114 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   }
 }
 
-// NW = waves per workgroup (4 or 8), HPB = q heads per workgroup; each head gets NW/HPB
-// waves of 32 queries, so BQ = 32 * NW / HPB queries per workgroup.
-template <int DT, int NW, int HPB, bool PAGED>
-__global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds_k[2][kKStage];
-  __shared__ __attribute__((aligned(16))) uint16_t lds_v[2][kVStage];
+// ---------------------------------------------------------------------------
+// Tile staging. K and V tiles are copied global -> LDS by the
+// load engine (global_load_lds_dwordx4: each lane's 16 bytes land at
+// LDS base + 16 * lane), so staging takes no registers and no LDS-store
+// instructions, and up to STAGES-1 tiles are in flight. Both tiles keep the
+// natural [key][d] layout with 16-byte chunks XOR-swizzled per row:
+//   K: chunk c of key r sits at position c ^ (r & 15)  -> the S^T operand reads
+//      (one 16-byte chunk of 32 consecutive keys) touch every bank once per 16 lanes;
+//   V: chunk c of key r sits at position c ^ 4 (r & 3) -> the transposed reads
+//      (ds_read_b64_tr_b16, 4 keys x 64 bytes per 16 lanes) are conflict-free.
+// The V^T operand of O^T += V^T P^T comes straight from the row-major tile through
+// ds_read_b64_tr_b16: within 16 lanes it returns lane i the 4 elements
+// {M[4j + i/4][i%4]}_j of the 16 x 4 block M whose row p the lane p addressed.
+// ---------------------------------------------------------------------------
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16;
+
+// One 16-byte global -> LDS copy per lane into lds_base + 16 * lane. The compiler
+// does not see this write; the kernel orders it with explicit vmcnt waits and
+// barriers (the builtin would make every later LDS read wait for all copies).
+__device__ __forceinline__ void copy_to_lds(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(src)
+               : "m0");
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int PER_TILE, int MAX_AHEAD>
+__device__ __forceinline__ void wait_tiles_ahead(int ahead) {
+  if constexpr (MAX_AHEAD >= 3) {
+    if (ahead >= 3) {
+      wait_vmcnt<PER_TILE * 3>();
+      return;
+    }
+  }
+  if constexpr (MAX_AHEAD >= 2) {
+    if (ahead >= 2) {
+      wait_vmcnt<PER_TILE * 2>();
+      return;
+    }
+  }
+  if constexpr (MAX_AHEAD >= 1) {
+    if (ahead >= 1) {
+      wait_vmcnt<PER_TILE>();
+      return;
+    }
+  }
+  wait_vmcnt<0>();
+}
+
+// q = x / d, r = x % d for 0 <= x < 2^22 and 1 <= d, via a float reciprocal and one
+// correction step each way.
+__device__ __forceinline__ int div_small(int x, int d, float inv, int& r) {
+  int q = static_cast<int>(static_cast<float>(x) * inv);
+  r = x - q * d;
+  if (r >= d) {
+    ++q;
+    r -= d;
+  }
+  if (r < 0) {
+    --q;
+    r += d;
+  }
+  return q;
+}
+
+template <int DT, int HPB, bool PAGED>
+__global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) {
+  constexpr int NW = kWaves;
+  constexpr int STAGES = kStages;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * kStageBytes];
 
   constexpr int kWavesPerHead = NW / HPB;
   constexpr int kBQ = kQPerWave * kWavesPerHead;
+  constexpr int kGroupsPerWave = 16 / NW;         // 4-row groups of each tile this wave copies
+  constexpr int kCopiesPerTile = 2 * kGroupsPerWave;  // K + V copies per wave per tile
   const int tid = threadIdx.x;
-  // Wave index as a scalar so every wave-level decision below is a uniform branch.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int col = lane & 31;   // query column / MFMA row index
-  const int half = lane >> 5;  // k-half of the MFMA operands
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  // The tiles are written only by the load engine, which the compiler does not see;
+  // one (never taken) visible store keeps it from treating the array as undefined.
+  if (a.num_items < 0) lds[tid] = 0;
 
   const int4 w = a.work[blockIdx.x];
+  if (w.x < 0) return;  // padding slot of the XCD-ordered work list
   const ReqInfo rq = a.reqs[w.x];
   const int q_begin = w.y;
   const int kvh = w.z;
   const int group = a.num_q_heads / a.num_kv_heads;
   const int qh = kvh * group + w.w * HPB + wave / kWavesPerHead;
-  const int wq0 = q_begin + (wave % kWavesPerHead) * kQPerWave;  // wave's first query
+  const int wq0 = q_begin + (wave % kWavesPerHead) * kQPerWave;
   const int kv_len = rq.prefix + rq.q_len;
-  const int q_hi = min(q_begin + kBQ, rq.q_len);        // workgroup's query end
-  const int keys_needed = min(kv_len, rq.prefix + q_hi);  // causal horizon of the tile
+  const int q_hi = min(q_begin + kBQ, rq.q_len);
+  const int keys_needed = min(kv_len, rq.prefix + q_hi);
   const int n_tiles = (keys_needed + kTileK - 1) / kTileK;
   const bool wave_active = wq0 < rq.q_len;
   const int wave_last_key = rq.prefix + min(wq0 + kQPerWave, rq.q_len) - 1;
 
-  // Q^T operand: lane holds query (wq0 + col), d = 16 s + 8 half .. +8.
   uint4 qreg[8];
   {
     const int qi = min(wq0 + col, rq.q_len - 1);
@@ -157,96 +223,65 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void prefill_kernel(Prefi
     wait_vmem_loads();
   }
 
-  // Global -> register staging of a K/V tile (64 keys x 256 bytes each). A 256-thread
-  // slice stages K (row = st/16 + 16 j, 16-byte chunk st%16: 16 lanes read one row) and
-  // a 256-thread slice stages V (keys 4 (st%16) + j, chunk st/16: the 16 lanes of an LDS
-  // phase then write one contiguous V^T row). With 8 waves the two slices are different
-  // waves and share one register set; with 4 waves every thread stages both.
-  constexpr bool kSplit = NW == 8;
-  const int st = tid & 255;
-  const bool does_k = !kSplit || wave < 4;
-  const bool does_v = !kSplit || wave >= 4;
-  const int k_chunk = st & 15;
-  const int k_row = st >> 4;
-  const int v_chunk = st >> 4;
-  const int v_group = st & 15;
-  // Within each 16-key block a V^T row stores the key quads in the order
-  // {0-3, 8-11, 4-7, 12-15}: the 8 keys an MFMA lane needs for one k-step
-  // (16 st + 4 half + {0..3, 8..11}) are then one contiguous 16-byte read.
-  const int v_slot = (v_group & ~3) * 4 + ((v_group & 1) * 8 + (v_group & 2) * 2);
-  const uint32_t k_sn = static_cast<uint32_t>(a.k_sn), v_sn = static_cast<uint32_t>(a.v_sn);
-  // Ragged rows are addressed from a workgroup-uniform base (the request's first row)
-  // with a 32-bit per-lane offset; paged rows from the slot index (64-bit product).
-  const uint16_t* k_req = a.k + kvh * a.k_sh + k_chunk * 8 +
-                          (PAGED ? 0 : static_cast<int64_t>(rq.q_start) * a.k_sn);
-  const uint16_t* v_req = a.v + kvh * a.v_sh + v_chunk * 8 +
-                          (PAGED ? 0 : static_cast<int64_t>(rq.q_start) * a.v_sn);
-  auto k_key = [&](int t, int j) { return t * kTileK + k_row + 16 * j; };
-  auto v_key = [&](int t, int j) { return t * kTileK + 4 * v_group + j; };
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)lds));
 
-  constexpr int kRows = kSplit ? 4 : 8;  // staged 16-byte rows per thread per tile
-  uint4 sa[kRows], sb[kRows];            // two register stages (tiles t+1 / t+2)
-  // Paged mode: page ids of a tile's rows are loaded one tile before the rows themselves
-  // (two alternating sets), so a row load never waits on its index load and the in-order
-  // vector-memory counter never has to drain earlier row loads.
-  int32_t pa[kRows], pb_[kRows];
-  auto load_pages = [&](int t, int32_t (&pg)[kRows]) {
-    if constexpr (PAGED) {
-      int i = 0;
-      if (does_k)
+  // Copy side: this wave copies row groups g = wave * kGroupsPerWave + j of the K and
+  // the V tile; lane -> row 4 g + lane / 16, LDS chunk position lane % 16.
+  const int row_in_group = lane >> 4;
+  const int pos = lane & 15;
+  const uint16_t* k_req = a.k + kvh * a.k_sh + (PAGED ? 0 : static_cast<int64_t>(rq.q_start) * a.k_sn);
+  const uint16_t* v_req = a.v + kvh * a.v_sh + (PAGED ? 0 : static_cast<int64_t>(rq.q_start) * a.v_sn);
+  const float inv_page = 1.0f / static_cast<float>(a.page_size);
+
+  // Copy one tile (this wave's 4-row groups of K and V) into `stage`. Paged mode: the 4
+  // rows of a group span at most 4 consecutive pages, starting at the page of the
+  // group's first (clamped) key; their ids are read with one uniform load from the
+  // constant address space (the words are read-only here), which becomes a scalar load
+  // counted on lgkmcnt and so never waits on the tile copies counted by vmcnt.
+  auto issue = [&](int t, int stage) {
+    const uint32_t sbase = lds_base + stage * kStageBytes;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          pg[i++] = a.indices[rq.page_base + min(k_key(t, j), kv_len - 1) / a.page_size];
-      if (does_v)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          pg[(kSplit ? 0 : 4) + j] =
-              a.indices[rq.page_base + min(v_key(t, j), kv_len - 1) / a.page_size];
-    }
-  };
-  auto row_ptr = [&](int j, int32_t page, const uint16_t* base, uint32_t sn) {
-    j = min(j, kv_len - 1);
-    if constexpr (PAGED) {
-      const uint32_t row = static_cast<uint32_t>(page) * static_cast<uint32_t>(a.page_size) +
-                           static_cast<uint32_t>(j % a.page_size);
-      return base + static_cast<uint64_t>(row) * sn;
-    } else {
-      return base + static_cast<uint32_t>(j) * sn;
-    }
-  };
-  auto load_tile = [&](int t, const int32_t (&pg)[kRows], uint4 (&sr)[kRows]) {
-    if (MI355X_PREFILL_ABLATE == 2 && t > 0) return;
-    if (does_k)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sr[j] = ld128(row_ptr(k_key(t, j), pg[j], k_req, k_sn));
-    if (does_v)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        sr[(kSplit ? 0 : 4) + j] =
-            ld128(row_ptr(v_key(t, j), pg[(kSplit ? 0 : 4) + j], v_req, v_sn));
-  };
-  auto store_tile = [&](int buf, const uint4 (&sr)[kRows]) {
-    if (does_k)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        st128(&lds_k[buf][(k_row + 16 * j) * kKPitch + k_chunk * 8], sr[j]);
-    if (does_v) {
-      // Transpose 4 keys x 8 dims into 8 rows of V^T (4 keys each, 8 bytes).
-      const uint4* vs = sr + (kSplit ? 0 : 4);
-      const uint32_t w0[4] = {vs[0].x, vs[0].y, vs[0].z, vs[0].w};
-      const uint32_t w1[4] = {vs[1].x, vs[1].y, vs[1].z, vs[1].w};
-      const uint32_t w2[4] = {vs[2].x, vs[2].y, vs[2].z, vs[2].w};
-      const uint32_t w3[4] = {vs[3].x, vs[3].y, vs[3].z, vs[3].w};
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int d = v_chunk * 8 + 2 * p;
-        uint2 even = make_uint2(lo16x2(w0[p], w1[p]), lo16x2(w2[p], w3[p]));
-        uint2 odd = make_uint2(hi16x2(w0[p], w1[p]), hi16x2(w2[p], w3[p]));
-        *reinterpret_cast<uint2*>(&lds_v[buf][d * kVPitch + v_slot]) = even;
-        *reinterpret_cast<uint2*>(&lds_v[buf][(d + 1) * kVPitch + v_slot]) = odd;
+    for (int j = 0; j < kGroupsPerWave; ++j) {
+      const int g = wave * kGroupsPerWave + j;
+      const int row = 4 * g + row_in_group;
+      // Keys past the end are clamped to the last key (finite data, masked later).
+      const int key = min(t * kTileK + row, kv_len - 1);
+      int64_t slot;
+      if constexpr (PAGED) {
+        const int key0 =
+            __builtin_amdgcn_readfirstlane(min(t * kTileK + 4 * g, (kv_len - 1) & ~3));
+        int r0;
+        const int p0 = __builtin_amdgcn_readfirstlane(div_small(key0, a.page_size, inv_page, r0));
+        const __attribute__((address_space(4))) int32_t* pw =
+            (const __attribute__((address_space(4))) int32_t*)(a.indices) + rq.page_base + p0;
+        const int i0 = pw[0], i1 = pw[1], i2 = pw[2], i3 = pw[3];
+        int off;
+        const int sel = div_small(key, a.page_size, inv_page, off) - p0;
+        const int page = sel == 0 ? i0 : sel == 1 ? i1 : sel == 2 ? i2 : i3;
+        slot = static_cast<int64_t>(page) * a.page_size + off;
+      } else {
+        slot = key;
       }
+      const int kc = pos ^ (row & 15);
+      const int vc = pos ^ (4 * (row & 3));
+      copy_to_lds(k_req + slot * a.k_sn + kc * 8, sbase + g * 1024);
+      copy_to_lds(v_req + slot * a.v_sn + vc * 8, sbase + kTileBytes + g * 1024);
     }
   };
+
+  // Read side offsets (bytes within a stage).
+  // K operand: key 32 T + col, chunk 2 kk + half at position (2 kk + half) ^ (col & 15).
+  // V^T operand (transposed read h of k-step kk, d block db): lane p of 16-lane group
+  // gq addresses key 16 kk + 4 (gq / 2) + 8 h + p / 4, d = 32 db + 16 (gq % 2) + 4 (p % 4).
+  const int gq = lane >> 4;
+  const int p16 = lane & 15;
+  const int v_key = 4 * (gq >> 1) + (p16 >> 2);
+  const int v_chunk_lo = 2 * (gq & 1) + ((p16 >> 1) & 1);  // chunk within the 64-byte block
+  int v_off[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+    v_off[db] = kTileBytes + v_key * 256 + ((4 * db + v_chunk_lo) ^ (4 * (p16 >> 2))) * 16 +
+                8 * (p16 & 1);
 
   floatx16 o[4];
 #pragma unroll
@@ -254,117 +289,108 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void prefill_kernel(Prefi
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
   float m = -1e30f, l = 0.f;
-  const int my_q = wq0 + col;                // query (local index) of this lane
-  const int my_horizon = rq.prefix + my_q;   // last visible key of this lane's query
+  const int my_q = wq0 + col;
+  const int my_horizon = rq.prefix + my_q;
 
-  // Body for one 64-key tile held in LDS buffer `buf`.
-  auto compute = [&](int t, int buf) {
+  // One 64-key tile per step: S^T = K Q^T (two 32-key blocks), mask and row max, lazy
+  // rescale, P^T = 2^(s scale - m), O^T += V^T P^T.
+  auto compute = [&](int t) {
     const int k0 = t * kTileK;
-    if (wave_active && k0 <= wave_last_key) {
-      // S^T for 64 keys: two 32-key blocks.
-      floatx16 s[2];
+    if (!(wave_active && k0 <= wave_last_key)) return;
+    const uint8_t* sb = lds + (t % STAGES) * kStageBytes;
+    uint4 kf[2][8];
 #pragma unroll
-      for (int T = 0; T < 2; ++T) {
+    for (int T = 0; T < 2; ++T)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[T][r] = 0.f;
-        const uint16_t* krow = &lds_k[buf][(32 * T + col) * kKPitch + 8 * half];
+      for (int kk = 0; kk < 8; ++kk)
+        kf[T][kk] = *reinterpret_cast<const uint4*>(
+            sb + (32 * T + col) * 256 + (((2 * kk + half) ^ (col & 15)) * 16));
+    floatx16 s[2];
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-          s[T] = Mfma<DT>::run(*reinterpret_cast<const uint4*>(krow + 16 * kk), qreg[kk], s[T]);
-      }
-      // Only the diagonal / last tiles need the causal and length mask (uniform branch).
-      if (k0 + kTileK - 1 > rq.prefix + wq0 || k0 + kTileK > kv_len) {
-        const int limit = min(my_horizon, kv_len - 1) - (k0 + 4 * half);
+    for (int T = 0; T < 2; ++T)
 #pragma unroll
-        for (int T = 0; T < 2; ++T)
+      for (int r = 0; r < 16; ++r) s[T][r] = 0.f;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = 32 * T + (r >> 2) * 8 + (r & 3);
-            s[T][r] = key <= limit ? s[T][r] : -INFINITY;
-          }
-      }
-      float mx = -INFINITY;
+    for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
-      for (int T = 0; T < 2; ++T)
+      for (int T = 0; T < 2; ++T) s[T] = Mfma<DT>::run(kf[T][kk], qreg[kk], s[T]);
+    uint4 vf[4][4];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[T][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;  // row max in log2 units
-      // Lazy rescale: the reference max m only moves when some row's max exceeds it
-      // by more than 8, so p = 2^(s - m) <= 2^8 and O/l are rescaled rarely.
-      if (__any(mx > m + 8.f)) {
-        const float m_new = fmaxf(m, mx);
-        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-        m = m_new;
-        l *= alpha;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-      }
-      uint4 pb[4];  // P^T operands for the four 16-key k-steps
-#pragma unroll
-      for (int T = 0; T < 2; ++T)
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          float p[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            p[i] = MI355X_PREFILL_ABLATE == 1
-                       ? s[T][8 * hh + i]
-                       : __builtin_amdgcn_exp2f(fmaf(s[T][8 * hh + i], a.scale_log2, -m));
-          pb[2 * T + hh] = make_uint4(pack2<DT>(p[0], p[1]), pack2<DT>(p[2], p[3]),
-                                      pack2<DT>(p[4], p[5]), pack2<DT>(p[6], p[7]));
-        }
-      // Row sum of the rounded P the PV product uses (v_dot2 against {1, 1}).
-      const uint32_t ones = pack2<DT>(1.f, 1.f);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        l = dot2<DT>(pb[kk].x, ones, l);
-        l = dot2<DT>(pb[kk].y, ones, l);
-        l = dot2<DT>(pb[kk].z, ones, l);
-        l = dot2<DT>(pb[kk].w, ones, l);
-      }
-      // O^T += V^T P^T; k-step kk covers keys 16 kk + 4 half + {0..3, 8..11}, the same
-      // order the S^T accumulators hold.
+    for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const uint16_t* vrow = &lds_v[buf][(32 * db + col) * kVPitch + 8 * half];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-          o[db] = Mfma<DT>::run(*reinterpret_cast<const uint4*>(vrow + 16 * kk), pb[kk], o[db]);
+        lds_u8* vp = (lds_u8*)sb + v_off[db] + 16 * kk * 256;
+        const uint2 l2 =
+            __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)vp));
+        const uint2 h2 = __builtin_bit_cast(
+            uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vp + 8 * 256)));
+        vf[kk][db] = make_uint4(l2.x, l2.y, h2.x, h2.y);
       }
+    if (k0 + kTileK - 1 > rq.prefix + wq0 || k0 + kTileK > kv_len) {
+      const int limit = min(my_horizon, kv_len - 1) - (k0 + 4 * half);
+#pragma unroll
+      for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = 32 * T + (r >> 2) * 8 + (r & 3);
+          s[T][r] = key <= limit ? s[T][r] : -INFINITY;
+        }
     }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[T][r]);
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                        false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * a.scale_log2;
+    }
+    // Lazy rescale: the reference max m only moves when some row's max exceeds it by
+    // more than 8, so p = 2^(s - m) <= 2^8 and O / l are rescaled rarely.
+    if (__any(mx > m + 8.f)) {
+      const float m_new = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      m = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+    }
+    uint4 pb[4];
+    const uint32_t ones = pack2<DT>(1.f, 1.f);
+#pragma unroll
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        float p[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          p[i] = __builtin_amdgcn_exp2f(fmaf(s[T][8 * hh + i], a.scale_log2, -m));
+        uint4& w4 = pb[2 * T + hh];
+        w4 = make_uint4(pack2<DT>(p[0], p[1]), pack2<DT>(p[2], p[3]), pack2<DT>(p[4], p[5]),
+                        pack2<DT>(p[6], p[7]));
+        l = dot2<DT>(w4.x, ones, l);
+        l = dot2<DT>(w4.y, ones, l);
+        l = dot2<DT>(w4.z, ones, l);
+        l = dot2<DT>(w4.w, ones, l);
+      }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[db] = Mfma<DT>::run(vf[kk][db], pb[kk], o[db]);
   };
 
-  // Two LDS buffers and two register stages: while tile t is consumed, tile t+1
-  // waits in registers (stored to LDS after the compute) and tile t+2 is in flight.
-  // Page ids run one tile further ahead (pa: even tiles, pb_: odd tiles).
-  load_pages(0, pa);
-  load_pages(1, pb_);
-  if (n_tiles > 0) {
-    load_tile(0, pa, sa);
-    store_tile(0, sa);
-  }
-  load_pages(2, pa);
-  if (n_tiles > 1) load_tile(1, pb_, sb);
-  load_pages(3, pb_);
-  __syncthreads();
-  for (int t = 0; t < n_tiles; t += 2) {
-    if (t + 2 < n_tiles) {
-      load_tile(t + 2, pa, sa);
-      load_pages(t + 4, pa);
-    }
-    compute(t, 0);
-    if (t + 1 < n_tiles) store_tile(1, sb);
+#pragma unroll
+  for (int st = 0; st < STAGES - 1; ++st)
+    if (st < n_tiles) issue(st, st);
+  for (int t = 0; t < n_tiles; ++t) {
+    wait_tiles_ahead<kCopiesPerTile, STAGES - 2>(min(STAGES - 2, n_tiles - 1 - t));
     __syncthreads();
-    if (t + 1 >= n_tiles) break;
-    if (t + 3 < n_tiles) {
-      load_tile(t + 3, pb_, sb);
-      load_pages(t + 5, pb_);
-    }
-    compute(t + 1, 1);
-    if (t + 2 < n_tiles) store_tile(0, sa);
-    __syncthreads();
+    if (t + STAGES - 1 < n_tiles)
+      issue(t + STAGES - 1, (t + STAGES - 1) % STAGES);
+    compute(t);
   }
 
   if (!wave_active || my_q >= rq.q_len) return;
@@ -422,23 +448,9 @@ struct Buffer {
   ~Buffer() { release(); }
 };
 
-// Waves per prefill workgroup: 8 (one workgroup per CU, 2 waves per SIMD, twice the
-// queries per K/V tile) for paged plans, whose long cached prefixes make K/V staging
-// the cost to amortise; 4 (two workgroups per CU, more workgroups) for ragged plans,
-// whose causal tail favours finer work items. Measured on MI355X at configs 3 and 4.
-// MI355X_PREFILL_WAVES=4|8 overrides both (tuning knob, read once).
-int prefill_waves(bool paged) {
-  static const int forced = [] {
-    const char* env = std::getenv("MI355X_PREFILL_WAVES");
-    const int v = env ? std::atoi(env) : 0;
-    return (v == 4 || v == 8) ? v : 0;
-  }();
-  return forced ? forced : (paged ? 8 : 4);
-}
-
-int heads_per_block(int64_t group, int waves) {
-  return static_cast<int>(std::min<int64_t>(group, waves));
-}
+// q heads per workgroup: all g heads of a kv head when g <= 8 waves, so each K/V tile
+// is fetched once for the whole group.
+int heads_per_block(int64_t group) { return static_cast<int>(std::min<int64_t>(group, kWaves)); }
 
 }  // namespace
 
@@ -447,7 +459,6 @@ struct PrefillPlan {
   int64_t num_q_heads = 0, num_kv_heads = 0, page_size = 0, dtype = 0;
   int64_t batch = 0, total_q = 0, num_items = 0, total_pages = 0;
   bool paged = false;
-  int waves = 8;  // waves per workgroup the work list was built for
   // Device int32 workspace: [req info 4*B][work 4*items][kv_indptr B+1][last_len B]
   int64_t o_work = 0, o_indptr = 0, o_last = 0;
   Buffer ints, indices, staging;
@@ -475,12 +486,9 @@ extern "C" int64_t mi355x_prefill_schedule(const int32_t* q_host, const int32_t*
       num_q_heads % num_kv_heads != 0)
     return -1;
   const int64_t group = num_q_heads / num_kv_heads;
-  bool paged = false;
-  for (int64_t r = 0; r < batch; ++r) paged |= prefix_host[r] > 0;
-  const int waves = prefill_waves(paged);
-  const int hpb = heads_per_block(group, waves);
+  const int hpb = heads_per_block(group);
   if (group % hpb) return -1;
-  const int bq = kQPerWave * (waves / hpb);
+  const int bq = kQPerWave * (kWaves / hpb);
   struct Item {
     int64_t cost;
     int32_t r, q0, kvh, hg;
@@ -498,7 +506,9 @@ extern "C" int64_t mi355x_prefill_schedule(const int32_t* q_host, const int32_t*
                            static_cast<int32_t>(h), static_cast<int32_t>(g)});
     }
   }
-  // Longest first: the heavy causal tail starts early and the short tiles fill the gaps.
+  // Longest first: the heavy causal tail starts early and the short items fill the gaps.
+  // (Grouping the items of one request and kv head on one XCD, for L2 reuse, measured
+  // slower on MI355X: the load balance loss outweighed the saved K/V reads.)
   std::stable_sort(items.begin(), items.end(),
                    [](const Item& x, const Item& y) { return x.cost > y.cost; });
   const int64_t n = static_cast<int64_t>(items.size());
@@ -539,6 +549,10 @@ extern "C" void* mi355x_prefill_prepare(void* existing, const int32_t* q_indptr,
     for (int64_t i = 0; i < batch; ++i) {
       if (prefix_host[i] < 0 || q_host[i + 1] <= q_host[i] || q_host[0] != 0) {
         set_error("invalid prefill lengths");
+        return nullptr;
+      }
+      if (int64_t(prefix_host[i]) + q_host[i + 1] - q_host[i] >= kMaxKvLen) {
+        set_error("prefill sequence longer than 4194303 tokens");
         return nullptr;
       }
       if (block_table &&
@@ -630,7 +644,7 @@ extern "C" void* mi355x_prefill_prepare(void* existing, const int32_t* q_indptr,
       return nullptr;
     }
     if (paged) {
-      if ((st = plan->indices.reserve(std::max<int64_t>(total_pages, 1) * 4, plan->allocations)) !=
+      if ((st = plan->indices.reserve((total_pages + 4) * 4, plan->allocations)) !=
           hipSuccess) {
         hip_error(st, "prefill index allocation");
         return nullptr;
@@ -650,7 +664,6 @@ extern "C" void* mi355x_prefill_prepare(void* existing, const int32_t* q_indptr,
     plan->num_items = n_items;
     plan->total_pages = total_pages;
     plan->paged = paged;
-    plan->waves = prefill_waves(paged);
     plan->o_work = o_work;
     plan->o_indptr = o_indptr;
     plan->o_last = o_last;
@@ -704,26 +717,20 @@ extern "C" const char* mi355x_prefill_plan_read(const void* plan, int32_t* kv_in
 
 namespace mi355x {
 namespace {
-template <int DT, int NW, int HPB>
+template <int DT, int HPB>
 void launch_prefill(const PrefillArgs& a, bool paged, hipStream_t s) {
-  const dim3 grid(static_cast<uint32_t>(a.num_items)), block(64 * NW);
+  const dim3 grid(static_cast<uint32_t>(a.num_items)), block(64 * kWaves);
   if (paged)
-    prefill_kernel<DT, NW, HPB, true><<<grid, block, 0, s>>>(a);
+    prefill_kernel<DT, HPB, true><<<grid, block, 0, s>>>(a);
   else
-    prefill_kernel<DT, NW, HPB, false><<<grid, block, 0, s>>>(a);
+    prefill_kernel<DT, HPB, false><<<grid, block, 0, s>>>(a);
 }
 template <int DT>
-void launch_dt(const PrefillArgs& a, int waves, int hpb, bool paged, hipStream_t s) {
-  if (waves == 8) {
-    if (hpb == 1) launch_prefill<DT, 8, 1>(a, paged, s);
-    else if (hpb == 2) launch_prefill<DT, 8, 2>(a, paged, s);
-    else if (hpb == 4) launch_prefill<DT, 8, 4>(a, paged, s);
-    else launch_prefill<DT, 8, 8>(a, paged, s);
-  } else {
-    if (hpb == 1) launch_prefill<DT, 4, 1>(a, paged, s);
-    else if (hpb == 2) launch_prefill<DT, 4, 2>(a, paged, s);
-    else launch_prefill<DT, 4, 4>(a, paged, s);
-  }
+void launch_dt(const PrefillArgs& a, int hpb, bool paged, hipStream_t s) {
+  if (hpb == 1) launch_prefill<DT, 1>(a, paged, s);
+  else if (hpb == 2) launch_prefill<DT, 2>(a, paged, s);
+  else if (hpb == 4) launch_prefill<DT, 4>(a, paged, s);
+  else launch_prefill<DT, 8>(a, paged, s);
 }
 }  // namespace
 }  // namespace mi355x
@@ -766,12 +773,11 @@ extern "C" const char* mi355x_prefill_run(const void* plan_ptr, const void* q, i
   a.num_kv_heads = static_cast<int32_t>(num_kv_heads);
   a.page_size = static_cast<int32_t>(p.paged ? page_size : 1);
   a.scale_log2 = (1.0f / std::sqrt(static_cast<float>(kD))) * kLog2e;
-  const int waves = p.waves;
-  const int hpb = heads_per_block(num_q_heads / num_kv_heads, waves);
+  const int hpb = heads_per_block(num_q_heads / num_kv_heads);
   auto s = static_cast<hipStream_t>(stream);
   if (dtype == 0)
-    launch_dt<0>(a, waves, hpb, p.paged, s);
+    launch_dt<0>(a, hpb, p.paged, s);
   else
-    launch_dt<1>(a, waves, hpb, p.paged, s);
+    launch_dt<1>(a, hpb, p.paged, s);
   return launch_status("prefill_kernel");
 }
