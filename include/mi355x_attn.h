@@ -189,9 +189,7 @@ const char* mi355x_prefill_plan_read(const void* plan, int32_t* kv_indptr, int32
                                      int32_t* last_len, void* stream);
 
 /* Host-only prefill work list: 4 ints per item {request, q_begin, kv_head,
- * head_group}. Items sharing a request and kv head are kept on one XCD (slot
- * i runs on XCD i % 8), longest causal horizon first within each XCD; slots
- * with request -1 are padding. work may be NULL to count.
+ * head_group}, longest causal horizon first. work may be NULL to count.
  * Returns the item count or -1. Stands in for FlashInfer's PrefillPlan
  * tiling (flashinfer_plan_run.cu:243-274). */
 int64_t mi355x_prefill_schedule(const int32_t* q_host, const int32_t* prefix_host, int64_t batch,
