@@ -127,9 +127,11 @@ const char* mi355x_decode_plan_read(const void* plan, int32_t* indptr, int32_t* 
                                     int32_t* last_len, int32_t* work, int32_t* merge,
                                     void* stream);
 
-/* Host-only split-KV scheduler used by mi355x_decode_prepare: fills `work`
- * (4 ints per item: request, token_begin, token_end, partial slot or -1) and
- * `merge` (2 ints per request: first partial slot or -1, chunk count).
+/* Host-only split-KV scheduler used by mi355x_decode_prepare (page size 1 view):
+ * every workgroup of the grid takes an equal share of all tokens (`chunk_tokens`
+ * receives the share); each request a share touches becomes one work item.
+ * Fills `work` (4 ints per item: request, token_begin, token_end, partial slot
+ * or -1) and `merge` (2 ints per request: first partial slot or -1, item count).
  * Returns the item count, or -1 on invalid input / insufficient capacity.
  * Stands in for FlashInfer's DecodePlan work estimation
  * (flashinfer_plan_run.cu:74-112). */
@@ -137,7 +139,7 @@ int64_t mi355x_decode_schedule(const int32_t* lengths, int64_t batch, int64_t cu
                                int64_t num_kv_heads, int32_t* work, int64_t work_capacity,
                                int32_t* merge, int64_t* chunk_tokens);
 
-/* Work-list capacity a plan reserves for `rows` requests. */
+/* Work-list capacity mi355x_decode_schedule needs for `rows` requests. */
 int64_t mi355x_decode_items_capacity(int64_t rows, int64_t cus, int64_t num_kv_heads);
 
 /* ------------------------------------------------------------------------

@@ -155,6 +155,54 @@ __device__ __forceinline__ void wait_vmem_loads() {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt=0, expcnt=7, lgkmcnt=15 (gfx9 encoding)
 }
 
+// ----------------------------------------------------------------------------
+// Direct global -> LDS copies (global_load_lds_dwordx4).
+// ----------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// LDS byte address of a __shared__ object (what m0 takes for the copies).
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_u8*)p));
+}
+
+// One 16-byte global -> LDS copy per lane into lds_base + 16 * lane. The compiler
+// does not see this write; the kernel orders it with explicit vmcnt waits and
+// barriers (the builtin would make every later LDS read wait for all copies).
+__device__ __forceinline__ void copy_to_lds(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(src)
+               : "m0");
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int PER_TILE, int MAX_AHEAD>
+__device__ __forceinline__ void wait_tiles_ahead(int ahead) {
+  if constexpr (MAX_AHEAD >= 3) {
+    if (ahead >= 3) {
+      wait_vmcnt<PER_TILE * 3>();
+      return;
+    }
+  }
+  if constexpr (MAX_AHEAD >= 2) {
+    if (ahead >= 2) {
+      wait_vmcnt<PER_TILE * 2>();
+      return;
+    }
+  }
+  if constexpr (MAX_AHEAD >= 1) {
+    if (ahead >= 1) {
+      wait_vmcnt<PER_TILE>();
+      return;
+    }
+  }
+  wait_vmcnt<0>();
+}
+
 // 128-bit global loads/stores.
 __device__ __forceinline__ uint4 ld128(const void* p) {
   return *reinterpret_cast<const uint4*>(p);

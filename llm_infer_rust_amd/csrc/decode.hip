@@ -16,16 +16,20 @@
 //   indices[indptr[r] + c] = block_table[r * stride + c], c < ceil(len[r] / P)
 //   last_page_len[r] = (len[r] - 1) % P + 1
 //
-// Split-KV schedule (our own design for 256 CUs): every request's tokens are cut
-// into chunks of `chunk_tokens` (a multiple of 16) chosen so that the number of
-// (request, chunk) work items is about 4 per CU. One workgroup handles one work
-// item for up to 8 KV heads (one wave per KV head), so the 2 KiB K row and the
-// 2 KiB V row of a page-size-1 slot are fetched by one workgroup at the same
-// time. A request that fits one chunk writes its output directly; others
-// write normalised fp32 partials + log2-sum-exp that a small merge kernel
-// combines. (Merging inside the last-arriving workgroup needs an agent-scope
-// release per workgroup, i.e. an L2 write-back on every XCD, and measured ~5x
-// slower than the extra launch.)
+// Split-KV schedule (our own design for 256 CUs): the grid's workgroups each take
+// an equal share of all tokens of the batch ("stream-K" over the flattened token
+// list); the requests a share touches become its work items. A request held by one
+// item writes its output directly; a request cut into several items writes
+// normalised fp32 partials + log2-sum-exp that a small merge kernel combines.
+// (Merging inside the last-arriving workgroup needs an agent-scope release per
+// workgroup, i.e. an L2 write-back on every XCD, and measured ~5x slower than the
+// extra launch.)
+//
+// Kernels. decode_dma_kernel (kv-head slices of 4 or 8 heads, the common case):
+// one 8-wave workgroup per CU streams 16-token tiles of whole K and V rows into a
+// 2-deep LDS ring with direct global -> LDS copies; wave w computes kv head w.
+// decode_kernel (other head counts): one wave per kv head loads its 256-byte row
+// slices straight into registers.
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -43,6 +47,12 @@ constexpr int kHeadDim = 128;
 constexpr int kTokensPerLaneGroup = 4;  // tokens per 16-lane group per loop trip
 constexpr int kTileTokens = 32;  // chunk granularity: a multiple of every tile size (4 * U)
 constexpr int kMaxWavesPerBlock = 8;
+// decode_dma_kernel shape (measured on MI355X at configs 2 and 5: 16-token tiles in a
+// 2-deep ring, one 8-wave workgroup per CU, beat 8-token tiles with 3-4 stages and
+// 4-wave workgroups two per CU).
+constexpr int kDmaTile = 16;           // tokens per LDS tile
+constexpr int kDmaStages = 2;          // LDS ring depth
+constexpr int kDmaMaxEntries = 2048;   // page entries of one work item held in LDS
 constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------------------
@@ -88,18 +98,21 @@ struct DeviceBuffer {
 };
 
 // int32 workspace layout (device and pinned staging share it):
-//   [0]                  number of work items
+//   [0]                  number of workgroups (per kv-head slice)
+//   [1]                  number of work items
 //   [4, 4+B+1)           indptr
 //   [o_work, +4*cap)     work items {request, token_begin, token_end, partial}
 //   [o_merge, +2*B)      per-request {first partial, chunk count}
+//   [o_wg, +wgs+1)       first work item of each workgroup
 struct IntLayout {
-  int64_t o_indptr, o_work, o_merge, total;
-  static IntLayout make(int64_t rows, int64_t items_cap) {
+  int64_t o_indptr, o_work, o_merge, o_wg, total;
+  static IntLayout make(int64_t rows, int64_t items_cap, int64_t wg_cap) {
     IntLayout l{};
     l.o_indptr = 4;
     l.o_work = (l.o_indptr + rows + 1 + 3) / 4 * 4;
     l.o_merge = l.o_work + 4 * items_cap;
-    l.total = l.o_merge + 2 * rows;
+    l.o_wg = l.o_merge + 2 * rows;
+    l.total = l.o_wg + wg_cap + 1;
     return l;
   }
 };
@@ -113,6 +126,7 @@ struct DecodePlan {
   int64_t graph_rows = 0, graph_columns = 0;
   // Current plan facts.
   int64_t batch = 0, total_pages = 0, num_items = 0, chunk_tokens = 0, items_capacity = 0;
+  int64_t num_wgs = 0, wg_capacity = 0;
   int64_t cus = 0;
   IntLayout layout{};
   DeviceBuffer ints, indices, last_len, partial_o, partial_lse;
@@ -165,47 +179,127 @@ int64_t target_items_for(int64_t cus, int64_t num_kv_heads) {
   return std::max<int64_t>(1, cus * per_cu / grid_y);
 }
 
-int64_t items_capacity_for(int64_t rows, int64_t cus, int64_t num_kv_heads) {
-  return rows + target_items_for(cus, num_kv_heads);
+// decode_dma_kernel for kv-head slices of 4 or 8 heads (tuning knobs, read once:
+// MI355X_DECODE_DMA=0 selects decode_kernel everywhere, MI355X_DECODE_DMA_W=4|8
+// forces the slice width).
+bool dma_enabled() {
+  static const bool on = [] {
+    const char* env = std::getenv("MI355X_DECODE_DMA");
+    return !(env && std::strcmp(env, "0") == 0);
+  }();
+  return on;
 }
 
-// Fills work (4 ints per item) and merge (2 ints per request). Returns the item
-// count, or -1 when `capacity` is too small.
-int64_t schedule(const int32_t* lengths, int64_t batch, int64_t cus, int64_t num_kv_heads,
-                 int32_t* work, int64_t capacity, int32_t* merge, int64_t* chunk_out) {
-  int64_t total = 0, longest = 0;
-  for (int64_t r = 0; r < batch; ++r) {
-    total += lengths[r];
-    longest = std::max<int64_t>(longest, lengths[r]);
-  }
-  const int64_t target = target_items_for(cus, num_kv_heads);
-  int64_t chunk;
-  if (batch >= target) {
-    chunk = longest;  // enough requests to fill the chip without splitting
+int64_t dma_lds_bytes(int64_t waves) {
+  return int64_t(kDmaStages) * 2 * kDmaTile * waves * 256 + int64_t(kDmaMaxEntries) * 4;
+}
+
+// How a decode launch is laid out for a kv-head count and page size.
+struct LaunchShape {
+  bool dma;            // decode_dma_kernel, else decode_kernel
+  int64_t waves;       // waves (kv heads) per workgroup
+  int64_t grid_y;      // kv-head slices
+  int64_t workgroups;  // split-KV workgroups per slice: the schedule's target
+  int64_t max_item;    // most tokens of one work item
+  int64_t wg_capacity;
+};
+
+LaunchShape launch_shape(int64_t cus, int64_t num_kv_heads, int64_t page_size) {
+  LaunchShape s{};
+  static const int64_t forced_w = [] {
+    const char* env = std::getenv("MI355X_DECODE_DMA_W");
+    const int v = env ? std::atoi(env) : 0;
+    return int64_t(v == 4 || v == 8 ? v : 0);
+  }();
+  const int64_t w =
+      forced_w && num_kv_heads % forced_w == 0 ? forced_w : std::min<int64_t>(num_kv_heads, kMaxWavesPerBlock);
+  s.dma = dma_enabled() && (w == 4 || w == 8) && num_kv_heads % w == 0;
+  if (s.dma) {
+    s.waves = w;
+    s.grid_y = num_kv_heads / w;
+    const int64_t per_cu = std::max<int64_t>(1, (160 * 1024) / dma_lds_bytes(w));
+    s.workgroups = std::max<int64_t>(1, cus * per_cu / s.grid_y);
+    s.max_item = int64_t(kDmaMaxEntries - 1) * page_size;  // its page entries fit in LDS
   } else {
-    const int64_t min_chunk = 128;
-    chunk = std::max<int64_t>((total + target - 1) / target, min_chunk);
-    chunk = (chunk + kTileTokens - 1) / kTileTokens * kTileTokens;
-    if (chunk >= longest) chunk = longest;
+    s.waves = waves_per_block(num_kv_heads);
+    s.grid_y = (num_kv_heads + s.waves - 1) / s.waves;
+    s.workgroups = target_items_for(cus, num_kv_heads);
+    s.max_item = std::numeric_limits<int32_t>::max();
   }
-  chunk = std::max<int64_t>(chunk, 1);
-  int64_t items = 0, partials = 0;
-  for (int64_t r = 0; r < batch; ++r) {
-    const int64_t len = lengths[r];
-    const int64_t n = (len + chunk - 1) / chunk;
-    merge[2 * r] = static_cast<int32_t>(n > 1 ? partials : -1);
-    merge[2 * r + 1] = static_cast<int32_t>(n);
-    for (int64_t c = 0; c < n; ++c) {
+  // Every workgroup but the last takes more than share - 32 >= 3/4 share tokens.
+  s.wg_capacity = s.workgroups + s.workgroups / 3 + 2;
+  return s;
+}
+
+// Items: one per request a share touches (<= workgroups + rows) plus the cuts at
+// max_item for rows of up to `row_tokens` tokens.
+int64_t items_capacity_for(const LaunchShape& s, int64_t rows, int64_t row_tokens) {
+  return s.wg_capacity + rows * (1 + (row_tokens + s.max_item - 1) / s.max_item);
+}
+
+// Balanced split-KV ("stream-K" over the flattened token list): the workgroups of
+// the grid each take an equal share of all tokens, walking the requests in order, so
+// every workgroup streams the same number of rows and the grid drains at once. A
+// workgroup's share becomes one work item per request it touches; a request cut into
+// several items gets normalised partials that the merge kernel combines, one held by
+// a single item writes its output directly. A share boundary that would leave fewer
+// than 32 tokens of a request is moved to the request end, and an item holds at most
+// `max_item` tokens.
+// Fills work (4 ints per item), merge (2 ints per request) and, when wg is not NULL,
+// wg[i] = first item of workgroup i (wg[workgroups] = item count). Returns the item
+// count, or -1 when a capacity is too small.
+int64_t schedule(const int32_t* lengths, int64_t batch, int64_t workgroups, int64_t max_item,
+                 int32_t* work, int64_t capacity, int32_t* merge, int64_t* share_out,
+                 int32_t* wg = nullptr, int64_t wg_capacity = 0, int64_t* wgs_out = nullptr) {
+  constexpr int64_t kMinShare = 128, kSliver = 32;
+  int64_t total = 0;
+  for (int64_t r = 0; r < batch; ++r) total += lengths[r];
+  int64_t share = std::max<int64_t>((total + workgroups - 1) / workgroups, kMinShare);
+  share = (share + kTileTokens - 1) / kTileTokens * kTileTokens;
+  int64_t items = 0, wgs = 0;
+  int64_t r = 0, pos = 0;
+  while (r < batch) {
+    if (wg) {
+      if (wgs >= wg_capacity) return -1;
+      wg[wgs] = static_cast<int32_t>(items);
+    }
+    ++wgs;
+    int64_t budget = share;
+    while (r < batch && budget > 0) {
+      const int64_t left = lengths[r] - pos;
+      int64_t take = std::min(budget, left);
+      if (left - take < kSliver) take = left;  // no sliver at the request end
+      take = std::min(take, max_item);
       if (items >= capacity) return -1;
       work[4 * items + 0] = static_cast<int32_t>(r);
-      work[4 * items + 1] = static_cast<int32_t>(c * chunk);
-      work[4 * items + 2] = static_cast<int32_t>(std::min(len, (c + 1) * chunk));
-      work[4 * items + 3] = static_cast<int32_t>(n > 1 ? partials + c : -1);
+      work[4 * items + 1] = static_cast<int32_t>(pos);
+      work[4 * items + 2] = static_cast<int32_t>(pos + take);
       ++items;
+      budget -= take;
+      pos += take;
+      if (pos == lengths[r]) {
+        ++r;
+        pos = 0;
+      }
+      if (budget < kSliver) break;  // no sliver at the share end
     }
-    if (n > 1) partials += n;
   }
-  *chunk_out = chunk;
+  if (wg) wg[wgs] = static_cast<int32_t>(items);
+  // Items of a request are consecutive: count them and assign partial slots.
+  int64_t partials = 0;
+  for (int64_t i = 0; i < items;) {
+    const int32_t req = work[4 * i];
+    int64_t n = 0;
+    while (i + n < items && work[4 * (i + n)] == req) ++n;
+    merge[2 * req] = static_cast<int32_t>(n > 1 ? partials : -1);
+    merge[2 * req + 1] = static_cast<int32_t>(n);
+    for (int64_t c = 0; c < n; ++c)
+      work[4 * (i + c) + 3] = static_cast<int32_t>(n > 1 ? partials + c : -1);
+    if (n > 1) partials += n;
+    i += n;
+  }
+  *share_out = share;
+  if (wgs_out) *wgs_out = wgs;
   return items;
 }
 
@@ -237,7 +331,7 @@ struct DecodeArgs {
   uint16_t* out;
   int64_t out_stride_n, out_stride_h;
   const int32_t* ints;  // workspace (num_items, indptr, work, merge)
-  int32_t o_indptr, o_work, o_merge;
+  int32_t o_indptr, o_work, o_merge, o_wg;
   const int32_t* indices;
   float* partial_o;
   float* partial_lse;
@@ -373,9 +467,10 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
   const int lane = threadIdx.x & 63;
   const int waves = blockDim.x >> 6;
   const int h = blockIdx.y * waves + wave;  // kv head
-  const int item = blockIdx.x;
-  if (item >= a.ints[0] || h >= a.num_kv_heads) return;  // graph plans launch a fixed capacity
-
+  const int wg = blockIdx.x;
+  if (wg >= a.ints[0] || h >= a.num_kv_heads) return;  // graph plans launch a fixed capacity
+  const int item_end = a.ints[a.o_wg + wg + 1];
+  for (int item = a.ints[a.o_wg + wg]; item < item_end; ++item) {
   const int4 w = reinterpret_cast<const int4*>(a.ints + a.o_work)[item];
   const int req = w.x, beg = w.y, end = w.z, pslot = w.w;
   const int grp = lane >> 4, sub = lane & 15;
@@ -441,7 +536,7 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
     m[gi] = mx;
     l[gi] = lv;
   }
-  if (grp != 0) return;
+  if (grp != 0) continue;
 #pragma unroll
   for (int gi = 0; gi < G; ++gi) {
     const int qh = h * G + gi;
@@ -455,6 +550,146 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
       if (sub == 0)  // log2-sum-exp of the chunk (v_log_f32 is log2)
         a.partial_lse[static_cast<int64_t>(pslot) * a.num_q_heads + qh] =
             m[gi] + __builtin_amdgcn_logf(l[gi]);
+    }
+  }
+}  // item loop
+}
+
+// ---------------------------------------------------------------------------
+// Decode with direct-to-LDS staging. One workgroup of W waves (one per kv head of
+// its head slice) per CU; the grid is the balanced split-KV schedule, so every
+// workgroup streams the same number of tokens. For each of its work items the
+// workgroup copies the item's page entries to LDS, then streams T-token tiles of
+// the K and V rows (W * 256 contiguous bytes per token and cache) through an
+// S-deep LDS ring with global_load_lds_dwordx4: the copies need no registers and
+// run S-1 tiles ahead of the math, and a page of P >= 4 tokens is read as long
+// contiguous runs. Wave w computes kv head w of the slice from LDS exactly as
+// decode_kernel does from registers.
+// ---------------------------------------------------------------------------
+template <int DT, int G, int W, int T, int S>
+__global__ __launch_bounds__(64 * W, 1) void decode_dma_kernel(DecodeArgs a) {
+  constexpr int kRow = W * 256;                 // bytes of one token's slice (K or V)
+  constexpr int kHalf = T * kRow;               // K (or V) bytes of one tile
+  constexpr int kStage = 2 * kHalf;
+  constexpr int kCopies = 2 * kHalf / 1024;     // 1 KiB copies per tile
+  constexpr int kPerWave = kCopies / W;
+  constexpr int U = T / 4;                      // tokens per 16-lane group per tile
+  static_assert(kRow >= 1024 && kRow % 1024 == 0, "a copy covers part of one token row");
+  static_assert(kCopies % W == 0 && U % 2 == 0, "tile shape");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[S * kStage];
+  __shared__ int32_t entries[kDmaMaxEntries];
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int grp = lane >> 4, sub = lane & 15;
+  const int h = blockIdx.y * W + wave;  // kv head
+  const int wg = blockIdx.x;
+  if (wg >= a.ints[0]) return;  // graph plans launch a fixed capacity
+  if (a.num_kv_heads < 0) lds[threadIdx.x] = 0;  // the copies are invisible to the compiler
+  const uint32_t lds_base = lds_address(lds);
+  const uint32_t row_elems = static_cast<uint32_t>(a.num_kv_heads) * kHeadDim;
+  const uint16_t* kslice = a.k_cache + blockIdx.y * W * kHeadDim;
+  const uint16_t* vslice = a.v_cache + blockIdx.y * W * kHeadDim;
+  const int item_end = a.ints[a.o_wg + wg + 1];
+
+  for (int item = a.ints[a.o_wg + wg]; item < item_end; ++item) {
+    const int4 wi = reinterpret_cast<const int4*>(a.ints + a.o_work)[item];
+    const int req = wi.x, beg = wi.y, end = wi.z, pslot = wi.w;
+    // Page entries of tokens [beg, end) -> LDS (the previous item's readers are done).
+    const int first_page = beg / a.page_size;
+    const int n_entries = (end - 1) / a.page_size - first_page + 1;
+    const int32_t* pages = a.indices + a.ints[a.o_indptr + req] + first_page;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n_entries; i += blockDim.x) entries[i] = pages[i];
+    uint4 qv[G];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi)
+      qv[gi] = ld128(a.q + req * a.q_stride_n + (h * G + gi) * a.q_stride_h + sub * 8);
+    wait_vmem_loads();
+    __syncthreads();
+
+    const int n_tiles = (end - beg + T - 1) / T;
+    // Copy c of a tile: half c / (kCopies / 2) (K, V), token (c % (kCopies / 2)) * 1024 /
+    // kRow of the tile, byte (c * 1024) % kRow of its row; the token is wave-uniform.
+    auto issue = [&](int t, int stage) {
+#pragma unroll
+      for (int j = 0; j < kPerWave; ++j) {
+        const int c = wave * kPerWave + j;
+        const int half = c / (kCopies / 2);
+        const int r = c % (kCopies / 2);
+        const int tok = min(beg + t * T + (r * 1024) / kRow, end - 1);
+        const int e = entries[tok / a.page_size - first_page];
+        const uint32_t slot = static_cast<uint32_t>(e) * static_cast<uint32_t>(a.page_size) +
+                              static_cast<uint32_t>(tok % a.page_size);
+        const uint16_t* src = (half ? vslice : kslice) + static_cast<uint64_t>(slot) * row_elems +
+                              ((r * 1024) % kRow) / 2 + lane * 8;
+        copy_to_lds(src, lds_base + stage * kStage + half * kHalf + r * 1024);
+      }
+    };
+
+    float m[G], l[G], o[G][8];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      m[gi] = -1e30f;
+      l[gi] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[gi][i] = 0.f;
+    }
+#pragma unroll
+    for (int st = 0; st < S - 1; ++st)
+      if (st < n_tiles) issue(st, st);
+    for (int t = 0; t < n_tiles; ++t) {
+      wait_tiles_ahead<kPerWave, S - 2>(min(S - 2, n_tiles - 1 - t));
+      __syncthreads();
+      if (t + S - 1 < n_tiles) issue(t + S - 1, (t + S - 1) % S);
+      const uint8_t* sb = lds + (t % S) * kStage + wave * 256 + sub * 16;
+      uint4 kr[U], vr[U];
+      bool ok[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int tt = 4 * u + grp;
+        kr[u] = *reinterpret_cast<const uint4*>(sb + tt * kRow);
+        vr[u] = *reinterpret_cast<const uint4*>(sb + kHalf + tt * kRow);
+        ok[u] = beg + t * T + tt < end;
+      }
+      consume<DT, G, U>(qv, kr, vr, ok, a.scale_log2, m, l, o);
+    }
+
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      float mx = fmaxf(m[gi], __shfl_xor(m[gi], 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float f = __builtin_amdgcn_exp2f(m[gi] - mx);
+      float lv = l[gi] * f;
+      lv += __shfl_xor(lv, 16);
+      lv += __shfl_xor(lv, 32);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float x = o[gi][i] * f;
+        x += __shfl_xor(x, 16);
+        x += __shfl_xor(x, 32);
+        o[gi][i] = x / lv;
+      }
+      m[gi] = mx;
+      l[gi] = lv;
+    }
+    if (grp == 0) {
+#pragma unroll
+      for (int gi = 0; gi < G; ++gi) {
+        const int qh = h * G + gi;
+        if (pslot < 0) {
+          st128(a.out + req * a.out_stride_n + qh * a.out_stride_h + sub * 8, pack8<DT>(o[gi]));
+        } else {
+          float* dst = a.partial_o +
+                       (static_cast<int64_t>(pslot) * a.num_q_heads + qh) * kHeadDim + sub * 8;
+          *reinterpret_cast<float4*>(dst) = make_float4(o[gi][0], o[gi][1], o[gi][2], o[gi][3]);
+          *reinterpret_cast<float4*>(dst + 4) =
+              make_float4(o[gi][4], o[gi][5], o[gi][6], o[gi][7]);
+          if (sub == 0)
+            a.partial_lse[static_cast<int64_t>(pslot) * a.num_q_heads + qh] =
+                m[gi] + __builtin_amdgcn_logf(l[gi]);
+        }
+      }
     }
   }
 }
@@ -545,6 +780,25 @@ bool dispatch_group(const DecodeArgs& a, int group, dim3 grid, int waves, bool p
   }
 }
 
+template <int DT, int G>
+void launch_dma(const DecodeArgs& a, dim3 grid, int waves, hipStream_t s) {
+  if (waves == 8)
+    decode_dma_kernel<DT, G, 8, kDmaTile, kDmaStages><<<grid, dim3(8 * kWave), 0, s>>>(a);
+  else
+    decode_dma_kernel<DT, G, 4, kDmaTile, kDmaStages><<<grid, dim3(4 * kWave), 0, s>>>(a);
+}
+
+template <int DT>
+bool dispatch_dma(const DecodeArgs& a, int group, dim3 grid, int waves, hipStream_t s) {
+  switch (group) {
+    case 1: launch_dma<DT, 1>(a, grid, waves, s); return true;
+    case 2: launch_dma<DT, 2>(a, grid, waves, s); return true;
+    case 4: launch_dma<DT, 4>(a, grid, waves, s); return true;
+    case 8: launch_dma<DT, 8>(a, grid, waves, s); return true;
+    default: return false;
+  }
+}
+
 }  // namespace
 }  // namespace mi355x
 
@@ -558,12 +812,15 @@ extern "C" int64_t mi355x_decode_schedule(const int32_t* lengths, int64_t batch,
     return -1;
   for (int64_t r = 0; r < batch; ++r)
     if (lengths[r] <= 0) return -1;
-  return schedule(lengths, batch, cus, num_kv_heads, work, work_capacity, merge, chunk_tokens);
+  // The host-only view: page size 1 and no cap on item length.
+  const LaunchShape shape = launch_shape(cus, num_kv_heads, 1);
+  return schedule(lengths, batch, shape.workgroups, std::numeric_limits<int32_t>::max(), work,
+                  work_capacity, merge, chunk_tokens);
 }
 
 extern "C" int64_t mi355x_decode_items_capacity(int64_t rows, int64_t cus, int64_t num_kv_heads) {
   if (rows < 0 || cus <= 0 || num_kv_heads <= 0) return -1;
-  return items_capacity_for(rows, cus, num_kv_heads);
+  return launch_shape(cus, num_kv_heads, 1).wg_capacity + rows;
 }
 
 extern "C" void* mi355x_decode_prepare(void* existing, const int32_t* block_table,
@@ -660,8 +917,10 @@ extern "C" void* mi355x_decode_prepare(void* existing, const int32_t* block_tabl
       }
     }
 
-    const int64_t items_cap = items_capacity_for(batch, plan->cus, num_kv_heads);
-    const IntLayout layout = IntLayout::make(batch, items_cap);
+    const LaunchShape shape = launch_shape(plan->cus, num_kv_heads, page_size);
+    const int64_t items_cap = items_capacity_for(shape, batch, columns * page_size);
+    const int64_t wg_cap = shape.wg_capacity;
+    const IntLayout layout = IntLayout::make(batch, items_cap, wg_cap);
     const size_t int_bytes = layout.total * sizeof(int32_t);
     const size_t idx_bytes = static_cast<size_t>(batch) * columns * sizeof(int32_t);
     const size_t part_o_bytes = static_cast<size_t>(items_cap) * num_q_heads * kHeadDim * 4;
@@ -695,14 +954,16 @@ extern "C" void* mi355x_decode_prepare(void* existing, const int32_t* block_tabl
     for (int64_t r = 0; r < batch; ++r)
       indptr[r + 1] = indptr[r] + static_cast<int32_t>(
                                       (plan->host_lengths[r] + page_size - 1) / page_size);
-    int64_t chunk = 0;
-    const int64_t items = schedule(plan->host_lengths.data(), batch, plan->cus, num_kv_heads,
-                                   host + layout.o_work, items_cap, host + layout.o_merge, &chunk);
+    int64_t chunk = 0, wgs = 0;
+    const int64_t items = schedule(plan->host_lengths.data(), batch, shape.workgroups,
+                                   shape.max_item, host + layout.o_work, items_cap,
+                                   host + layout.o_merge, &chunk, host + layout.o_wg, wg_cap, &wgs);
     if (items < 0) {
       set_error("decode work list exceeds its capacity");
       return nullptr;
     }
-    host[0] = static_cast<int32_t>(items);
+    host[0] = static_cast<int32_t>(wgs);
+    host[1] = static_cast<int32_t>(items);
     st = hipMemcpyAsync(plan->ints.ptr, host, int_bytes, hipMemcpyHostToDevice, s);
     if (st != hipSuccess) {
       hip_error(st, "decode metadata upload");
@@ -726,6 +987,8 @@ extern "C" void* mi355x_decode_prepare(void* existing, const int32_t* block_tabl
     plan->num_items = items;
     plan->chunk_tokens = chunk;
     plan->items_capacity = items_cap;
+    plan->num_wgs = wgs;
+    plan->wg_capacity = wg_cap;
     plan->layout = layout;
     created.release();
     return plan;
@@ -808,6 +1071,7 @@ extern "C" const char* mi355x_decode_run(const void* plan_ptr, const void* q, in
   a.o_indptr = static_cast<int32_t>(p.layout.o_indptr);
   a.o_work = static_cast<int32_t>(p.layout.o_work);
   a.o_merge = static_cast<int32_t>(p.layout.o_merge);
+  a.o_wg = static_cast<int32_t>(p.layout.o_wg);
   a.indices = static_cast<const int32_t*>(p.indices.ptr);
   a.partial_o = static_cast<float*>(p.partial_o.ptr);
   a.partial_lse = static_cast<float*>(p.partial_lse.ptr);
@@ -816,15 +1080,19 @@ extern "C" const char* mi355x_decode_run(const void* plan_ptr, const void* q, in
   a.page_size = static_cast<int32_t>(page_size);
   a.scale_log2 = (1.0f / std::sqrt(static_cast<float>(kHeadDim))) * kLog2e;
 
-  const int waves = static_cast<int>(waves_per_block(num_kv_heads));
-  const int64_t grid_y = (num_kv_heads + waves - 1) / waves;
+  const LaunchShape shape = launch_shape(p.cus, num_kv_heads, page_size);
+  const int waves = static_cast<int>(shape.waves);
   // Graph plans launch the fixed capacity; surplus workgroups exit at once.
-  const int64_t grid_x = p.graph ? p.items_capacity : p.num_items;
-  const dim3 grid(static_cast<uint32_t>(grid_x), static_cast<uint32_t>(grid_y));
+  const int64_t grid_x = p.graph ? p.wg_capacity : p.num_wgs;
+  const dim3 grid(static_cast<uint32_t>(grid_x), static_cast<uint32_t>(shape.grid_y));
   const int group = static_cast<int>(num_q_heads / num_kv_heads);
   auto s = static_cast<hipStream_t>(stream);
-  const bool ok = dtype == 0 ? dispatch_group<0>(a, group, grid, waves, page_size == 1, s)
-                             : dispatch_group<1>(a, group, grid, waves, page_size == 1, s);
+  const bool ok =
+      shape.dma
+          ? (dtype == 0 ? dispatch_dma<0>(a, group, grid, waves, s)
+                        : dispatch_dma<1>(a, group, grid, waves, s))
+          : (dtype == 0 ? dispatch_group<0>(a, group, grid, waves, page_size == 1, s)
+                        : dispatch_group<1>(a, group, grid, waves, page_size == 1, s));
   if (!ok) return set_error("unsupported query group size");
   if (const char* err = launch_status("decode_kernel")) return err;
   if (p.graph || p.num_items > p.batch) {  // some request was split

@@ -122,46 +122,7 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 // ---------------------------------------------------------------------------
 
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16;
-
-// One 16-byte global -> LDS copy per lane into lds_base + 16 * lane. The compiler
-// does not see this write; the kernel orders it with explicit vmcnt waits and
-// barriers (the builtin would make every later LDS read wait for all copies).
-__device__ __forceinline__ void copy_to_lds(const void* src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(src)
-               : "m0");
-}
-
-// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in 15:14).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-template <int PER_TILE, int MAX_AHEAD>
-__device__ __forceinline__ void wait_tiles_ahead(int ahead) {
-  if constexpr (MAX_AHEAD >= 3) {
-    if (ahead >= 3) {
-      wait_vmcnt<PER_TILE * 3>();
-      return;
-    }
-  }
-  if constexpr (MAX_AHEAD >= 2) {
-    if (ahead >= 2) {
-      wait_vmcnt<PER_TILE * 2>();
-      return;
-    }
-  }
-  if constexpr (MAX_AHEAD >= 1) {
-    if (ahead >= 1) {
-      wait_vmcnt<PER_TILE>();
-      return;
-    }
-  }
-  wait_vmcnt<0>();
-}
 
 // q = x / d, r = x % d for 0 <= x < 2^22 and 1 <= d, via a float reciprocal and one
 // correction step each way.
@@ -223,7 +184,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
     wait_vmem_loads();
   }
 
-  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8*)lds));
+  const uint32_t lds_base = lds_address(lds);
 
   // Copy side: this wave copies row groups g = wave * kGroupsPerWave + j of the K and
   // the V tile; lane -> row 4 g + lane / 16, LDS chunk position lane % 16.

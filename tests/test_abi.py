@@ -69,8 +69,8 @@ def test_decode_schedule_config2_shape(native):
     lengths = rng.integers(512, 4097, size=64).tolist()
     n, work, merge, chunk, cap = _schedule(native, lengths)
     oplan.check_work_list(work, merge, lengths)
-    # enough items to fill 256 CUs, each a bounded slice of the KV
-    assert n >= 512
+    # at least one item per CU, each share a bounded slice of the KV
+    assert n >= 256
     assert chunk >= 128
 
 
