@@ -30,7 +30,7 @@ BF16_PEAK_TFLOPS = 2500.0
 COPY_CAL_BYTES = 256 << 20
 LAYERS = 4  # KV pools the decode steps rotate over (4 x 16 GiB)
 TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "decode_kernel_cfg2_traffic.txt")
+                               "decode_cfg2_traffic.txt")
 
 
 def measured_traffic():
@@ -112,7 +112,7 @@ def parse_args():
                    help="requests in the bounded CPU-baseline sample")
     p.add_argument("--decode-only", action="store_true",
                    help="skip the prefill and norm measurements")
-    p.add_argument("--only", choices=["prefill", "norms", "e2e"],
+    p.add_argument("--only", choices=["prefill", "norms", "e2e", "ceilings"],
                    help="print only this section's measurements (tuning aid)")
     p.add_argument("--e2e-requests", type=int, default=256)
     p.add_argument("--e2e-input", type=int, default=1024)
@@ -286,6 +286,71 @@ def prefill_sections(dev, reps: int) -> dict:
     return out
 
 
+def ceilings_section(dev, w, reps: int) -> dict:
+    """Measured ceilings of this GPU for the two bounds (llm_infer_rust_amd/calib/ceilings.hip):
+    the cfg2 decode memory pattern without arithmetic (random 2 KiB K and V rows at the same
+    slots, rotating over the same 4 pools), a contiguous read of the same byte count, bf16 MFMA
+    on random operands, and the prefill kernel's per-tile work on LDS-resident random tiles."""
+    import ctypes
+    from llm_infer_rust_amd import _native  # noqa: F401  (HIP runtime loaded by torch first)
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                   "llm_infer_rust_amd", "libmi355x_calib.so"))
+    for name in ("mi355x_calib_gather", "mi355x_calib_stream", "mi355x_calib_mfma",
+                 "mi355x_calib_attention_core"):
+        getattr(lib, name).restype = ctypes.c_char_p
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    lens = w["lengths"].tolist()
+    slots = torch.cat([w["table"][b, :n] for b, n in enumerate(lens)]).to(torch.int32).to(dev)
+    rows = int(slots.numel())
+    nbytes = rows * 2 * w["HKV"] * w["D"] * 2
+
+    def check(err):
+        if err:
+            raise RuntimeError(err.decode())
+
+    def gather(i):
+        check(lib.mi355x_calib_gather(ctypes.c_void_p(w["kcs"][i % LAYERS].data_ptr()),
+                                      ctypes.c_void_p(w["vcs"][i % LAYERS].data_ptr()),
+                                      ctypes.c_void_p(slots.data_ptr()), rows,
+                                      ctypes.c_void_p(sink.data_ptr()), stream))
+
+    def stream_read(i):
+        check(lib.mi355x_calib_stream(ctypes.c_void_p(w["kcs"][i % LAYERS].data_ptr()), nbytes,
+                                      ctypes.c_void_p(sink.data_ptr()), stream))
+
+    def timed(fn, n):
+        fn(0)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(n):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    out = {}
+    ms = timed(gather, reps)
+    out["gather_2k_rows"] = {"us": round(ms * 1e3, 2), "bytes": nbytes,
+                             "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    ms = timed(stream_read, reps)
+    out["stream_read"] = {"us": round(ms * 1e3, 2), "bytes": nbytes,
+                          "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    blocks, iters = 4096, 1024
+    ms = timed(lambda i: check(lib.mi355x_calib_mfma(blocks, iters,
+                                                     ctypes.c_void_p(sink.data_ptr()), stream)), 5)
+    flops = blocks * 8 * iters * 4 * 32768
+    out["mfma_bf16_random"] = {"TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}
+    blocks, iters = 1024, 400
+    ms = timed(lambda i: check(lib.mi355x_calib_attention_core(
+        blocks, iters, ctypes.c_void_p(sink.data_ptr()), stream)), 5)
+    flops = blocks * 8 * iters * 32 * 32768
+    out["attention_core_random"] = {"TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}
+    return out
+
+
 def norm_sections(dev, reps: int) -> dict:
     """cfg3 norms on 8192 x 1024 hidden rows and the 8192-token packed QKV (HBM-bound)."""
     from llm_infer_rust_amd import ops
@@ -361,7 +426,7 @@ def main():
     if args.only == "e2e":
         print(json.dumps({"e2e": e2e_section(dev, args)}))
         return
-    if args.only:
+    if args.only in ("prefill", "norms"):
         fn = prefill_sections if args.only == "prefill" else norm_sections
         print(json.dumps({args.only: fn(dev, max(args.steps, 20))}))
         return
@@ -373,6 +438,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     w = build_workload(args.seed, dev)
+    if args.only == "ceilings":
+        print(json.dumps({"ceilings": ceilings_section(dev, w, max(min(args.steps, 50), 5))}))
+        return
     B, HQ, HKV, D = w["B"], w["HQ"], w["HKV"], w["D"]
     caches = []
     for kc, vc in zip(w["kcs"], w["vcs"]):
@@ -449,7 +517,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
-                     "kernel": "decode_kernel+merge_kernel (one mi355x_decode_run)",
+                     "kernel": "decode_dma_kernel+merge_kernel (one mi355x_decode_run)",
                      "algorithmic_bytes": dbytes, "avg_launch_us": round(decode_ms * 1e3, 3)},
         "kv_store": {"us": round(store_ms * 1e3, 3), "bytes": sbytes,
                      "GB/s": round(sbytes / (store_ms * 1e-3) / 1e9, 2)},
@@ -460,6 +528,12 @@ def main():
     if not args.decode_only:
         result["prefill"] = prefill_sections(dev, reps)
         result["norms"] = norm_sections(dev, reps)
+        ceil = ceilings_section(dev, w, min(reps, 50))
+        ceil["decode_vs_gather"] = round(achieved / ceil["gather_2k_rows"]["GB/s"], 4)
+        core = ceil["attention_core_random"]["TFLOP/s"]
+        ceil["prefill_vs_core"] = {k: round(v["TFLOP/s"] / core, 4)
+                                   for k, v in result["prefill"].items()}
+        result["ceilings"] = ceil
     # The decode workload's 64 GiB of KV pools are released before the e2e model is built.
     del w, caches, plan, out, table_d, lens_d, meta, step, c
     torch.cuda.empty_cache()
