@@ -399,12 +399,19 @@ def norm_sections(dev, reps: int) -> dict:
         i = it[0] = it[0] + 1
         ops.add_rms_norm(dx[i % sets], dr[i % sets], w4, 1e-6)
 
+    # Reference point for these sizes: torch's device copy of the rms_norm bytes
+    # (16 MiB in, 16 MiB out), same buffer rotation.
+    def copy_ref():
+        i = it[0] = it[0] + 1
+        outs[i % sets].copy_(xs[i % sets])
+
     res = {}
     for name, fn, nbytes in (
             ("rms_norm", rms, 2 * 8192 * 1024 * 2),
             ("add_rms_norm", add_rms, 4 * 8192 * 1024 * 2),
             ("qk_norm", qk, 2 * 8192 * 24 * 128 * 2),
-            ("add_rms_norm_256x4096", add_rms_decode, 4 * 256 * 4096 * 2)):
+            ("add_rms_norm_256x4096", add_rms_decode, 4 * 256 * 4096 * 2),
+            ("torch_copy_16MiB_ref", copy_ref, 2 * 8192 * 1024 * 2)):
         ms = _event_time_ms(fn, reps)
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
