@@ -166,8 +166,14 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
   const int q_begin = w.y;
   const int kvh = w.z;
   const int group = a.num_q_heads / a.num_kv_heads;
-  const int qh = kvh * group + w.w * HPB + wave / kWavesPerHead;
-  const int wq0 = q_begin + (wave % kWavesPerHead) * kQPerWave;
+  // Waves w and w + 4 share a SIMD. The upper four waves take their (head, query slot)
+  // in mirrored order, so each SIMD pairs an early query slot with a late one and the
+  // causal tiles near the diagonal, where late slots still work and early ones are
+  // done, are spread over all four SIMDs.
+  static_assert(NW == 8, "mirrored slot order assumes 8 waves");
+  const int slot_id = wave >= 4 ? 11 - wave : wave;
+  const int qh = kvh * group + w.w * HPB + slot_id / kWavesPerHead;
+  const int wq0 = q_begin + (slot_id % kWavesPerHead) * kQPerWave;
   const int kv_len = rq.prefix + rq.q_len;
   const int q_hi = min(q_begin + kBQ, rq.q_len);
   const int keys_needed = min(kv_len, rq.prefix + q_hi);
@@ -255,10 +261,10 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
 
   // One 64-key tile per step: S^T = K Q^T (two 32-key blocks), mask and row max, lazy
   // rescale, P^T = 2^(s scale - m), O^T += V^T P^T.
-  auto compute = [&](int t) {
+  auto compute = [&](int t, int stage) {
     const int k0 = t * kTileK;
     if (!(wave_active && k0 <= wave_last_key)) return;
-    const uint8_t* sb = lds + (t % STAGES) * kStageBytes;
+    const uint8_t* sb = lds + stage * kStageBytes;
     uint4 kf[2][8];
 #pragma unroll
     for (int T = 0; T < 2; ++T)
@@ -346,12 +352,14 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
 #pragma unroll
   for (int st = 0; st < STAGES - 1; ++st)
     if (st < n_tiles) issue(st, st);
+  int read_stage = 0, fill_stage = STAGES - 1;  // ring positions of tile t and t + STAGES - 1
   for (int t = 0; t < n_tiles; ++t) {
     wait_tiles_ahead<kCopiesPerTile, STAGES - 2>(min(STAGES - 2, n_tiles - 1 - t));
     __syncthreads();
-    if (t + STAGES - 1 < n_tiles)
-      issue(t + STAGES - 1, (t + STAGES - 1) % STAGES);
-    compute(t);
+    if (t + STAGES - 1 < n_tiles) issue(t + STAGES - 1, fill_stage);
+    compute(t, read_stage);
+    read_stage = read_stage == STAGES - 1 ? 0 : read_stage + 1;
+    fill_stage = fill_stage == STAGES - 1 ? 0 : fill_stage + 1;
   }
 
   if (!wave_active || my_q >= rq.q_len) return;

@@ -184,3 +184,64 @@ def test_prefill_plan_reuse_and_errors(gpu):
     del batch
     with pytest.raises(ModelError, match="too small"):
         attn.prepare(meta_for(gpu, [0, 1, 2], [600, 0], table), 2)
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8), (8, 8)])
+def test_ragged_mixed_tiny_and_long_sequences(gpu, hq, hkv):
+    """One- and two-token sequences, sequences ending exactly on and just past a 64-key
+    tile or a query block, and longer ones in one batch (every row checked)."""
+    g = torch.Generator().manual_seed(100 + hq)
+    lens = [1, 64, 65, 2, 127, 128, 129, 300, 5, 33, 640, 1, 96, 200]
+    bounds = [0] + np.cumsum(lens).tolist()
+    n = bounds[-1]
+    q = randn((n, hq, 128), g, torch.bfloat16, gpu)
+    k = randn((n, hkv, 128), g, torch.bfloat16, gpu)
+    v = randn((n, hkv, 128), g, torch.bfloat16, gpu)
+    attn = make(gpu, hq, hkv, 16, torch.bfloat16)
+    table = torch.zeros(len(lens), 64, dtype=torch.int32, device=gpu)
+    batch = attn.prepare(meta_for(gpu, bounds, [0] * len(lens), table), n)
+    out = batch.forward(q, k, v, BaseAttention())
+    want = oatt.prefill_ragged(f32(q), f32(k), f32(v), bounds)
+    assert_close(f32(out).reshape(want.shape), want, f"hq={hq} hkv={hkv}")
+
+
+@pytest.mark.parametrize("seed", [1, 5])
+def test_paged_small_prefixes_and_tiny_extends(gpu, seed):
+    """Paged prefill with prefixes of 0 to a few pages (ending on and off page borders)
+    and extends of 1 to 130 tokens (page 16, Hq32/Hkv8, random page permutation); every
+    row checked."""
+    rng = np.random.default_rng(seed)
+    g = torch.Generator().manual_seed(seed)
+    page = 16
+    pref = np.array([0, 1, 15, 16, 63, 64, 200, 0, 31, 500])
+    ext = np.array([1, 1, 2, 70, 1, 64, 33, 130, 3, 1])
+    bounds = [0] + np.cumsum(ext).tolist()
+    pages_per = (pref + ext + page - 1) // page
+    cols = int(pages_per.max())
+    pool = int(pages_per.sum()) + 1
+    perm = rng.permutation(pool - 1) + 1
+    table = np.zeros((len(ext), cols), np.int32)
+    off = 0
+    for r in range(len(ext)):
+        table[r, : pages_per[r]] = perm[off: off + pages_per[r]]
+        off += pages_per[r]
+    kc = randn((pool, page, 8, 128), g, torch.bfloat16, gpu)
+    vc = randn((pool, page, 8, 128), g, torch.bfloat16, gpu)
+    n = bounds[-1]
+    q = randn((n, 32, 128), g, torch.bfloat16, gpu)
+    attn = make(gpu, 32, 8, page, torch.bfloat16)
+    cache = BaseAttention()
+    cache.bind_kv_cache(kc, vc)
+    batch = attn.prepare(meta_for(gpu, bounds, pref.tolist(), torch.from_numpy(table).to(gpu)), n)
+    assert batch.plan.plan.paged
+    out = f32(batch.forward(q, q, q, cache)).reshape(n, 32, 128)
+    flat_k = f32(kc).reshape(-1, 8, 128)
+    flat_v = f32(vc).reshape(-1, 8, 128)
+    qf = f32(q)
+    for r in range(len(ext)):
+        for i in range(int(ext[r])):
+            horizon = int(pref[r]) + i + 1
+            slots = oatt.slots_of(table[r], horizon, page)
+            want = oatt.attention_against_cache(qf[bounds[r] + i: bounds[r] + i + 1],
+                                                flat_k[slots], flat_v[slots], horizon - 1, 32, 8)
+            assert_close(out[bounds[r] + i], want[0], f"seed={seed} req={r} row={i}")
