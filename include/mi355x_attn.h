@@ -239,6 +239,27 @@ const char* mi355x_silu_mul(const void* gate_up, void* out, int64_t tokens, int6
                             int dtype, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Decode-batch projections.
+ * ------------------------------------------------------------------------ */
+
+/* out[M, N] = x[M, K] . w[N, K]^T (row strides ldx, ldw, ldo in elements),
+ * fp32 accumulation, one rounding. Meant for decode batches (M up to a few
+ * hundred rows); K % 64 == 0, N % 4 == 0, 16-byte aligned rows. When the
+ * chosen tiling splits K, the fp32 partials go to `workspace`
+ * (mi355x_linear_workspace_bytes tells how much). config / splits < 0 pick
+ * the tiling for `cus` compute units; otherwise they force one (tuning).
+ * Replaces the decode-time x.matmul(w.T) of src/layers/linear.rs:5-7. */
+const char* mi355x_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, void* out,
+                          int64_t ldo, int64_t M, int64_t N, int64_t K, void* workspace,
+                          int64_t workspace_bytes, int32_t cus, int32_t config, int32_t splits,
+                          int64_t dtype, void* stream);
+
+/* Workspace bytes mi355x_linear needs for this shape and tiling (0 when K is
+ * not split, -1 for an invalid shape). Host-only. */
+int64_t mi355x_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t cus,
+                                      int32_t config, int32_t splits);
+
+/* ------------------------------------------------------------------------
  * Sampling.
  * ------------------------------------------------------------------------ */
 

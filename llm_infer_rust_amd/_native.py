@@ -78,6 +78,10 @@ SIGNATURES: dict[str, tuple] = {
                                              c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                              c_i64, c_i64, c_i64, c_double, c_int, c_void_p]),
     "mi355x_silu_mul": (c_char_p, [c_void_p, c_void_p, c_i64, c_i64, c_int, c_void_p]),
+    "mi355x_linear": (c_char_p, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64,
+                                 c_i64, c_i64, c_void_p, c_i64, c_i32, c_i32, c_i32, c_i64,
+                                 c_void_p]),
+    "mi355x_linear_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i32, c_i32, c_i32]),
     "mi355x_sample": (c_char_p, [c_void_p, c_i64, c_i64, c_i64, c_int, c_void_p, c_void_p,
                                  c_void_p, c_u64, c_u64, c_void_p, c_void_p]),
 }
@@ -130,3 +134,14 @@ def dtype_code(t: torch.Tensor) -> int:
     if t.dtype == torch.float16:
         return 1
     raise NativeError(f"expected bfloat16 or float16 tensor, got {t.dtype}")
+
+
+_CUS: dict[int, int] = {}
+
+
+def device_cus(device: torch.device) -> int:
+    """Compute units of a GPU (cached per device index)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index not in _CUS:
+        _CUS[index] = torch.cuda.get_device_properties(index).multi_processor_count
+    return _CUS[index]

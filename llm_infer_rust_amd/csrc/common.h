@@ -182,6 +182,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 template <int PER_TILE, int MAX_AHEAD>
 __device__ __forceinline__ void wait_tiles_ahead(int ahead) {
+  static_assert(MAX_AHEAD <= 4 && PER_TILE * MAX_AHEAD < 64, "vmcnt range");
+  if constexpr (MAX_AHEAD >= 4) {
+    if (ahead >= 4) {
+      wait_vmcnt<PER_TILE * 4>();
+      return;
+    }
+  }
   if constexpr (MAX_AHEAD >= 3) {
     if (ahead >= 3) {
       wait_vmcnt<PER_TILE * 3>();

@@ -1,0 +1,367 @@
+// Decode-step projection GEMMs on gfx950: out[M, N] = x[M, K] . w[N, K]^T.
+//
+// Replaces the reference's `x.matmul(w.T)` (src/layers/linear.rs:5-7, cuBLAS through
+// tch) for the decoder layer's QKV, o_proj, gate_up and down projections and the
+// lm_head when the batch is a decode batch (M <= 256 rows). Prefill-sized products
+// stay on hipBLASLt, which already runs them near the MFMA rate.
+//
+// Why a kernel of its own: at M = 256 the four per-layer products carry 99 GFLOP
+// over 386 MB of weights, so they sit at the ridge between the MFMA rate and HBM
+// bandwidth, and their output (256 x N) is too small to give all 256 CUs a tile
+// with enough operand reuse. hipBLASLt's choices reach 1.2-3 TB/s here.
+//
+// Design:
+//   * one workgroup computes a BM x BN output tile over a K range (split-K when
+//     the tiles alone cannot fill the chip; fp32 partials, then a reduce kernel);
+//   * the x and w tiles of each 64-wide K step stream through a 3-deep LDS ring filled
+//     by direct global -> LDS copies (global_load_lds_dwordx4), rows of 128 bytes
+//     with the 16-byte chunks XOR-swizzled so the MFMA operand reads are
+//     conflict-free;
+//   * each wave owns a (32 a) x (32 b) block of the transposed product
+//     D[n][m] = sum_k w[n][k] x[m][k] and runs v_mfma_f32_32x32x16 with A = w rows and
+//     B = x rows, so each lane ends up with 4 consecutive output columns per
+//     accumulator quad (8-byte stores);
+//   * workgroups that share a weight tile (different M tiles of it) are placed on the
+//     same XCD (workgroup i runs on XCD i mod 8), so the tile is fetched from HBM once.
+#include <algorithm>
+#include <cstdint>
+
+#include "common.h"
+
+namespace mi355x {
+namespace {
+
+typedef __bf16 lin_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 lin_f16x8_t __attribute__((ext_vector_type(8)));
+typedef float lin_floatx16 __attribute__((ext_vector_type(16)));
+
+template <int DT>
+__device__ __forceinline__ lin_floatx16 mfma32(const uint4& a, const uint4& b, lin_floatx16 c) {
+  if constexpr (DT == 0)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(lin_bf16x8_t, a),
+                                                   __builtin_bit_cast(lin_bf16x8_t, b), c, 0, 0,
+                                                   0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(lin_f16x8_t, a),
+                                                  __builtin_bit_cast(lin_f16x8_t, b), c, 0, 0, 0);
+}
+
+constexpr int kBK = 64;            // K elements per ring stage
+constexpr int kRowBytes = kBK * 2;  // one tile row of a stage
+
+struct LinearArgs {
+  const uint16_t* x;
+  const uint16_t* w;
+  uint16_t* out;
+  float* partial;  // [splits][M][N] fp32 when splits > 1
+  int64_t ldx, ldw, ldo;
+  int32_t M, N, K;
+  int32_t splits, k_per_split;  // k_per_split is a multiple of kBK
+  int32_t tiles_m, tiles_n, groups;  // groups = tiles_n * splits rounded up to 8
+};
+
+// Swizzled position of 16-byte chunk c in tile row r: c ^ f(r) with
+// f(r) = (r & 7) ^ ((r >> 3) & 1). Any 8 consecutive rows (aligned) put a given chunk
+// in 8 different positions, and over 16 rows the (row parity, position) pairs are all
+// distinct, so 32 lanes reading one chunk of 32 rows hit every bank evenly.
+__device__ __forceinline__ int chunk_pos(int c, int r) { return c ^ ((r & 7) ^ ((r >> 3) & 1)); }
+
+template <int DT, int BM, int BN, int WM, int WN, int STAGES, bool PARTIAL>
+__global__ __launch_bounds__(64 * WM * WN, 1) void linear_kernel(LinearArgs a) {
+  constexpr int NW = WM * WN;
+  constexpr int kWaveM = BM / WM, kWaveN = BN / WN;  // wave tile
+  constexpr int A_BLK = kWaveN / 32, B_BLK = kWaveM / 32;
+  static_assert(kWaveM % 32 == 0 && kWaveN % 32 == 0, "wave tile must be 32-aligned");
+  constexpr int kGroups = (BM + BN) / 8;  // 8-row (1 KB) copy groups per stage
+  static_assert(kGroups % NW == 0, "copy groups must split evenly over the waves");
+  constexpr int kCopies = kGroups / NW;  // copy instructions per wave per stage
+  constexpr int kStageBytes = (BM + BN) * kRowBytes;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * kStageBytes];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  if (a.M < 0) lds[tid] = 0;  // never taken; the copies' LDS writes are invisible
+
+  // Workgroup -> (M tile, N tile, split). The M tiles of one (N tile, split) are
+  // consecutive multiples of 8 apart, i.e. on one XCD at about the same time.
+  const int b = blockIdx.x;
+  const int xcd = b & 7;
+  const int rest = b >> 3;
+  const int tm = rest % a.tiles_m;
+  const int lin = (rest / a.tiles_m) * 8 + xcd;
+  if (lin >= a.tiles_n * a.splits) return;
+  const int tn = lin % a.tiles_n;
+  const int split = lin / a.tiles_n;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int k_begin = split * a.k_per_split;
+  const int n_k = min(a.k_per_split, a.K - k_begin) / kBK;
+
+  const uint32_t lds_base = lds_address(lds);
+  // Copy side: group g = wave + NW * j covers tile rows 8 g .. 8 g + 7 (x rows first,
+  // then w rows); lane -> row 8 g + lane / 8, position lane % 8.
+  const uint16_t* src[kCopies];
+  uint32_t dst[kCopies];
+#pragma unroll
+  for (int j = 0; j < kCopies; ++j) {
+    const int g = wave + NW * j;
+    const int row = 8 * g + (lane >> 3);
+    const int pos = lane & 7;
+    if (8 * g < BM) {
+      const int m = min(m0 + row, a.M - 1);
+      src[j] = a.x + static_cast<int64_t>(m) * a.ldx + k_begin + chunk_pos(pos, row) * 8;
+    } else {
+      const int r = row - BM;
+      const int n = min(n0 + r, a.N - 1);
+      src[j] = a.w + static_cast<int64_t>(n) * a.ldw + k_begin + chunk_pos(pos, r) * 8;
+    }
+    dst[j] = lds_base + g * 1024;
+  }
+  auto issue = [&](int t, int stage) {
+#pragma unroll
+    for (int j = 0; j < kCopies; ++j) copy_to_lds(src[j] + t * kBK, dst[j] + stage * kStageBytes);
+  };
+
+  const int wm = wave % WM, wn = wave / WM;
+  const int col = lane & 31, half = lane >> 5;
+  lin_floatx16 acc[A_BLK][B_BLK];
+#pragma unroll
+  for (int i = 0; i < A_BLK; ++i)
+#pragma unroll
+    for (int j = 0; j < B_BLK; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // All operand fragments of a stage are read before its MFMAs (a scheduling barrier
+  // keeps the compiler from interleaving them to save registers), so each MFMA waits
+  // only for reads issued a whole k-step earlier rather than the one just before it.
+  auto compute = [&](int stage) {
+    const uint8_t* sb = lds + stage * kStageBytes;
+    uint4 af[kBK / 16][A_BLK], bf[kBK / 16][B_BLK];
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      const int c = 2 * kk + half;
+#pragma unroll
+      for (int i = 0; i < A_BLK; ++i) {
+        const int r = wn * kWaveN + 32 * i + col;
+        af[kk][i] =
+            *reinterpret_cast<const uint4*>(sb + (BM + r) * kRowBytes + chunk_pos(c, r) * 16);
+      }
+#pragma unroll
+      for (int j = 0; j < B_BLK; ++j) {
+        const int r = wm * kWaveM + 32 * j + col;
+        bf[kk][j] = *reinterpret_cast<const uint4*>(sb + r * kRowBytes + chunk_pos(c, r) * 16);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk)
+#pragma unroll
+      for (int i = 0; i < A_BLK; ++i)
+#pragma unroll
+        for (int j = 0; j < B_BLK; ++j) acc[i][j] = mfma32<DT>(af[kk][i], bf[kk][j], acc[i][j]);
+  };
+
+#pragma unroll
+  for (int st = 0; st < STAGES - 1; ++st)
+    if (st < n_k) issue(st, st);
+  int read_stage = 0, fill_stage = STAGES - 1;
+  for (int t = 0; t < n_k; ++t) {
+    wait_tiles_ahead<kCopies, STAGES - 2>(min(STAGES - 2, n_k - 1 - t));
+    __syncthreads();
+    if (t + STAGES - 1 < n_k) issue(t + STAGES - 1, fill_stage);
+    compute(read_stage);
+    read_stage = read_stage == STAGES - 1 ? 0 : read_stage + 1;
+    fill_stage = fill_stage == STAGES - 1 ? 0 : fill_stage + 1;
+  }
+
+  // Lane holds D[n][m] for m = column `col` of each B block and n = 8 q + 4 half + e
+  // (e = 0..3) of each A block, accumulator elements 4 q + e.
+#pragma unroll
+  for (int j = 0; j < B_BLK; ++j) {
+    const int m = m0 + wm * kWaveM + 32 * j + col;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int i = 0; i < A_BLK; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * kWaveN + 32 * i + 8 * q + 4 * half;
+        if (n >= a.N) continue;
+        const float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                            acc[i][j][4 * q + 3]};
+        if constexpr (PARTIAL) {
+          float* p = a.partial + (static_cast<int64_t>(split) * a.M + m) * a.N + n;
+          *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+          const uint2 packed = make_uint2(Elem<DT>::pack2(v[0], v[1]), Elem<DT>::pack2(v[2], v[3]));
+          *reinterpret_cast<uint2*>(a.out + static_cast<int64_t>(m) * a.ldo + n) = packed;
+        }
+      }
+  }
+}
+
+// out[m][n..n+3] = sum over splits of partial[s][m][n..n+3], rounded once.
+template <int DT>
+__global__ __launch_bounds__(256) void linear_reduce(const float* __restrict__ partial,
+                                                     uint16_t* __restrict__ out, int64_t ldo,
+                                                     int M, int N, int splits) {
+  const int64_t quads = static_cast<int64_t>(M) * (N / 4);
+  const int64_t plane = static_cast<int64_t>(M) * N;
+  for (int64_t i = blockIdx.x * int64_t(256) + threadIdx.x; i < quads;
+       i += int64_t(gridDim.x) * 256) {
+    const int m = static_cast<int>(i / (N / 4));
+    const int n = static_cast<int>(i % (N / 4)) * 4;
+    float4 s = *reinterpret_cast<const float4*>(partial + static_cast<int64_t>(m) * N + n);
+    for (int k = 1; k < splits; ++k) {
+      const float4 t =
+          *reinterpret_cast<const float4*>(partial + k * plane + static_cast<int64_t>(m) * N + n);
+      s.x += t.x;
+      s.y += t.y;
+      s.z += t.z;
+      s.w += t.w;
+    }
+    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(m) * ldo + n) =
+        make_uint2(Elem<DT>::pack2(s.x, s.y), Elem<DT>::pack2(s.z, s.w));
+  }
+}
+
+struct TileConfig {
+  int bm, bn, wm, wn, stages;
+};
+
+// The compiled tile shapes (waves arranged wm x wn over the tile).
+constexpr TileConfig kConfigs[] = {
+    {128, 192, 4, 2, 4},  // wave 32 x 96
+    {128, 128, 4, 2, 5},  // wave 32 x 64
+    {256, 128, 4, 2, 3},  // wave 64 x 64
+    {128, 256, 4, 2, 3},  // wave 32 x 128
+    {64, 256, 2, 4, 4},   // wave 32 x 64
+    {256, 64, 8, 1, 4},   // wave 32 x 64
+    {128, 128, 4, 2, 3},  // wave 32 x 64, shallow ring
+    {64, 128, 2, 4, 5},   // wave 32 x 32
+};
+constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
+
+template <int DT, int C, bool PARTIAL>
+void launch_config(const LinearArgs& a, int blocks, hipStream_t s) {
+  constexpr TileConfig t = kConfigs[C];
+  linear_kernel<DT, t.bm, t.bn, t.wm, t.wn, t.stages, PARTIAL>
+      <<<dim3(blocks), dim3(64 * t.wm * t.wn), 0, s>>>(a);
+}
+
+template <int DT, int C>
+void launch_any(const LinearArgs& a, int blocks, hipStream_t s) {
+  if (a.splits > 1)
+    launch_config<DT, C, true>(a, blocks, s);
+  else
+    launch_config<DT, C, false>(a, blocks, s);
+}
+
+template <int DT>
+void launch_dt(int config, const LinearArgs& a, int blocks, hipStream_t s) {
+  switch (config) {
+    case 0: launch_any<DT, 0>(a, blocks, s); break;
+    case 1: launch_any<DT, 1>(a, blocks, s); break;
+    case 2: launch_any<DT, 2>(a, blocks, s); break;
+    case 3: launch_any<DT, 3>(a, blocks, s); break;
+    case 4: launch_any<DT, 4>(a, blocks, s); break;
+    case 5: launch_any<DT, 5>(a, blocks, s); break;
+    case 6: launch_any<DT, 6>(a, blocks, s); break;
+    default: launch_any<DT, 7>(a, blocks, s); break;
+  }
+}
+
+struct Choice {
+  int config, splits;
+};
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Tile shape and split count: for each tile shape in order of preference, the fewest
+// K splits that give at least 3/4 of a workgroup per CU; the first shape that needs at
+// most 4 splits wins, else the one needing the fewest. Measured on MI355X at the
+// Qwen3-8B decode shapes (M = 1..256): 128 x 128 tiles with up to 4 splits beat smaller
+// tiles with fewer splits, most clearly on the long-K down projection.
+Choice choose(int64_t M, int64_t N, int64_t K, int cus) {
+  const int order[] = {6, 0, 7};
+  const int64_t want = (3 * int64_t(cus)) / 4;
+  Choice best{-1, 1 << 30};
+  for (int c : order) {
+    const TileConfig& t = kConfigs[c];
+    const int64_t tiles = ceil_div(M, t.bm) * ceil_div(N, t.bn);
+    int s = 1;
+    while (s < 8 && tiles * s < want && K % (int64_t(2 * s) * kBK) == 0) s *= 2;
+    if (K % (int64_t(s) * kBK)) continue;
+    if (s <= 4) return {c, s};
+    if (s < best.splits) best = {c, s};
+  }
+  return best.config >= 0 ? best : Choice{7, 1};
+}
+
+}  // namespace
+}  // namespace mi355x
+
+using namespace mi355x;
+
+// Workspace bytes (fp32 split-K partials) that mi355x_linear needs for this shape.
+extern "C" int64_t mi355x_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t cus,
+                                                 int32_t config, int32_t splits) {
+  if (M <= 0 || N <= 0 || K <= 0) return -1;
+  Choice c = config >= 0 ? Choice{config, splits} : choose(M, N, K, cus > 0 ? cus : 256);
+  return c.splits > 1 ? int64_t(c.splits) * M * N * 4 : 0;
+}
+
+extern "C" const char* mi355x_linear(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                     void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                                     void* workspace, int64_t workspace_bytes, int32_t cus,
+                                     int32_t config, int32_t splits, int64_t dtype,
+                                     void* stream) {
+  if (!x || !w || !out) return set_error("mi355x_linear: null pointer");
+  if (M <= 0 || N <= 0 || K <= 0 || M > 4096 || N % 4 || K % kBK || ldx < K || ldw < K ||
+      ldo < N || ldx % 8 || ldw % 8 || ldo % 4 || (dtype != 0 && dtype != 1))
+    return set_error("mi355x_linear: unsupported shape (K % 64, N % 4, 16-byte rows)");
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 8))
+    return set_error("mi355x_linear: misaligned operand");
+  Choice c = config >= 0 ? Choice{config, splits} : choose(M, N, K, cus > 0 ? cus : 256);
+  if (c.config < 0 || c.config >= kNumConfigs || c.splits < 1 || K % (int64_t(c.splits) * kBK))
+    return set_error("mi355x_linear: invalid tile configuration");
+  const TileConfig& t = kConfigs[c.config];
+  if (c.splits > 1) {
+    if (!workspace || workspace_bytes < int64_t(c.splits) * M * N * 4 || !aligned(workspace, 16))
+      return set_error("mi355x_linear: split-K workspace too small");
+  }
+  LinearArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(w);
+  a.out = static_cast<uint16_t*>(out);
+  a.partial = static_cast<float*>(workspace);
+  a.ldx = ldx;
+  a.ldw = ldw;
+  a.ldo = ldo;
+  a.M = static_cast<int32_t>(M);
+  a.N = static_cast<int32_t>(N);
+  a.K = static_cast<int32_t>(K);
+  a.splits = c.splits;
+  a.k_per_split = static_cast<int32_t>(K / c.splits);
+  a.tiles_m = static_cast<int32_t>(ceil_div(M, t.bm));
+  a.tiles_n = static_cast<int32_t>(ceil_div(N, t.bn));
+  a.groups = static_cast<int32_t>(ceil_div(int64_t(a.tiles_n) * a.splits, 8) * 8);
+  const int64_t blocks = int64_t(a.groups) * a.tiles_m;
+  if (blocks > (int64_t(1) << 31) - 1) return set_error("mi355x_linear: grid too large");
+  auto s = static_cast<hipStream_t>(stream);
+  if (dtype == 0)
+    launch_dt<0>(c.config, a, static_cast<int>(blocks), s);
+  else
+    launch_dt<1>(c.config, a, static_cast<int>(blocks), s);
+  if (const char* e = launch_status("linear_kernel")) return e;
+  if (c.splits > 1) {
+    const int64_t quads = M * (N / 4);
+    const int grid = static_cast<int>(std::min<int64_t>(ceil_div(quads, 256), 4096));
+    if (dtype == 0)
+      linear_reduce<0><<<grid, 256, 0, s>>>(a.partial, a.out, ldo, a.M, a.N, c.splits);
+    else
+      linear_reduce<1><<<grid, 256, 0, s>>>(a.partial, a.out, ldo, a.M, a.N, c.splits);
+    if (const char* e = launch_status("linear_reduce")) return e;
+  }
+  return nullptr;
+}

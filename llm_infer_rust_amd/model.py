@@ -183,17 +183,17 @@ class Qwen3Model:
                 x = ops.rms_norm(hidden, layer.input_layernorm, eps)
             else:
                 x, residual = ops.add_rms_norm(hidden, residual, layer.input_layernorm, eps)
-            qkv = F.linear(x, layer.qkv_proj)
+            qkv = ops.linear(x, layer.qkv_proj)
             q = qkv[:, : hq * d].view(t, hq, d)
             k = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
             v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
             ops.qk_norm_rope_store(q, k, v, layer.q_norm, layer.k_norm, eps, positions,
                                    self.rope, layer.base_attention, write_loc)
             attn = attention_batch.forward(q, k, v, layer.base_attention)
-            o = F.linear(attn, layer.o_proj)
+            o = ops.linear(attn, layer.o_proj)
             x, residual = ops.add_rms_norm(o, residual, layer.post_attention_layernorm, eps)
-            gate_up = F.linear(x, layer.gate_up_proj)
-            hidden = F.linear(ops.silu_and_mul(gate_up), layer.down_proj)
+            gate_up = ops.linear(x, layer.gate_up_proj)
+            hidden = ops.linear(ops.silu_and_mul(gate_up), layer.down_proj)
         hidden, _ = ops.add_rms_norm(hidden, residual, self.norm, eps)
         if logits_indices is not None:
             hidden = hidden.index_select(0, logits_indices)

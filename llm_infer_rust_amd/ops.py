@@ -212,5 +212,66 @@ def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         stream_of(q)), "qk_norm_rope_store")
 
 
+# Decode batches (at most this many rows) with an output of at most DECODE_MAX_N
+# columns go to the gfx950 projection kernel; long-K products (K > 4096) only from
+# DECODE_LONG_K_MIN_ROWS rows up. Everything else stays on hipBLASLt through
+# F.linear. The bounds come from timing both on MI355X at the Qwen3-8B shapes: the
+# kernel wins on QKV, o_proj and down (1.2-2.8x at 64-256 rows); hipBLASLt keeps
+# gate_up, the lm_head and prefill-sized products.
+DECODE_MAX_ROWS = 256
+DECODE_MAX_N = 8192
+DECODE_LONG_K_MIN_ROWS = 32
+
+
+def uses_decode_kernel(rows: int, n: int, k: int) -> bool:
+    """Whether ``linear`` routes an ``[rows, k] x [n, k]^T`` product to the gfx950 kernel."""
+    return (rows <= DECODE_MAX_ROWS and n <= DECODE_MAX_N and n % 4 == 0 and k % 64 == 0
+            and (k <= 4096 or rows >= DECODE_LONG_K_MIN_ROWS))
+
+
+def decode_linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,
+                  config: int = -1, splits: int = -1) -> torch.Tensor:
+    """``x @ weight.T`` on the gfx950 projection kernel (fp32 accumulation, one rounding).
+
+    x ``[M, K]`` with unit column stride, weight ``[N, K]`` contiguous, same 16-bit
+    dtype. When the kernel splits K, its fp32 partials live in a workspace taken from
+    the caching allocator (safe under HIP graph capture). ``config``/``splits`` force a
+    tiling (tuning and tests); -1 lets the library choose. Replaces the decode-time
+    ``x.matmul(w.T)`` of ``src/layers/linear.rs:5-7``."""
+    _require_device(x, "decode_linear")
+    dt = dtype_code(x)
+    if (x.dim() != 2 or weight.dim() != 2 or x.stride(1) != 1 or not weight.is_contiguous()
+            or weight.dtype != x.dtype or weight.device != x.device
+            or weight.size(1) != x.size(1)):
+        raise NativeError("invalid linear operands: expected x [M, K] and weight [N, K]")
+    m, k = x.shape
+    n = weight.size(0)
+    if out is None:
+        out = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    elif (out.shape != (m, n) or out.dtype != x.dtype or out.stride(1) != 1
+          or out.device != x.device):
+        raise NativeError("invalid linear output")
+    cus = _native.device_cus(x.device)
+    need = lib().mi355x_linear_workspace_bytes(m, n, k, cus, config, splits)
+    if need < 0:
+        raise NativeError("invalid linear shape")
+    ws = torch.empty(max(int(need), 16), dtype=torch.uint8, device=x.device) if need else None
+    check(lib().mi355x_linear(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                              out.data_ptr(), out.stride(0), m, n, k,
+                              None if ws is None else ws.data_ptr(), int(need), cus, config,
+                              splits, dt, stream_of(x)), "decode_linear")
+    return out
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """``x @ weight.T``: decode-sized products on the gfx950 kernel, the rest on
+    hipBLASLt (``src/layers/linear.rs:5-7``)."""
+    if (x.is_cuda and x.dim() == 2 and x.stride(1) == 1 and weight.is_contiguous()
+            and uses_decode_kernel(x.size(0), weight.size(0), x.size(1))):
+        return decode_linear(x, weight)
+    return torch.nn.functional.linear(x, weight)
+
+
 __all__ = ["rms_norm", "add_rms_norm", "qk_norm", "silu_and_mul", "HalfSplitRope", "rope",
-           "qk_norm_rope_store", "NativeError", "_native"]
+           "qk_norm_rope_store", "decode_linear", "linear", "uses_decode_kernel", "NativeError",
+           "_native"]

@@ -83,3 +83,12 @@ def test_decode_schedule_rejects_bad_input(native):
     assert lib.mi355x_decode_schedule(lens, 2, 256, 8, work, 16, merge, ctypes.byref(chunk)) == -1
     lens = (ctypes.c_int32 * 1)(10**6)
     assert lib.mi355x_decode_schedule(lens, 1, 256, 8, work, 1, merge, ctypes.byref(chunk)) == -1
+
+
+def test_linear_workspace_bytes_query(native):
+    f = native.lib().mi355x_linear_workspace_bytes
+    assert f(256, 4096, 4096, 256, 6, 1) == 0
+    assert f(256, 4096, 4096, 256, 6, 4) == 4 * 256 * 4096 * 4
+    assert f(0, 4096, 4096, 256, -1, -1) == -1
+    # the library's own choice for the Qwen3-8B down projection splits K
+    assert f(256, 4096, 12288, 256, -1, -1) > 0
