@@ -254,6 +254,21 @@ const char* mi355x_linear(const void* x, int64_t ldx, const void* w, int64_t ldw
                           int64_t workspace_bytes, int32_t cus, int32_t config, int32_t splits,
                           int64_t dtype, void* stream);
 
+/* The projection fused with the residual RMSNorm that follows it in a decoder
+ * layer (o_proj -> post-attention norm, down -> next layer's input norm):
+ *   y = x . w^T (rounded once), residual <- round(y + residual),
+ *   out <- round(rms(y + residual) * norm_weight)   (norm on the fp32 sum).
+ * Equal bit for bit to mi355x_linear followed by mi355x_add_rms_norm; the
+ * split-K partials are reduced inside the norm pass instead of a separate
+ * launch. Width N: a multiple of 8 in 1032..8192 (rows of 16-byte chunks);
+ * library-chosen tiling, workspace as for mi355x_linear (config = splits = -1).
+ * Replaces linear.rs:5-7 followed by ops.rs:22-35 (fused_ops.cu:300-338). */
+const char* mi355x_linear_add_rms_norm(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                       void* residual, int64_t ldr, const void* norm_weight,
+                                       double eps, void* out, int64_t ldo, int64_t M, int64_t N,
+                                       int64_t K, void* workspace, int64_t workspace_bytes,
+                                       int32_t cus, int64_t dtype, void* stream);
+
 /* Workspace bytes mi355x_linear needs for this shape and tiling (0 when K is
  * not split, -1 for an invalid shape). Host-only. */
 int64_t mi355x_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t cus,

@@ -81,6 +81,10 @@ SIGNATURES: dict[str, tuple] = {
     "mi355x_linear": (c_char_p, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64,
                                  c_i64, c_i64, c_void_p, c_i64, c_i32, c_i32, c_i32, c_i64,
                                  c_void_p]),
+    "mi355x_linear_add_rms_norm": (c_char_p, [c_void_p, c_i64, c_void_p, c_i64, c_void_p,
+                                              c_i64, c_void_p, c_double, c_void_p, c_i64,
+                                              c_i64, c_i64, c_i64, c_void_p, c_i64, c_i32,
+                                              c_i64, c_void_p]),
     "mi355x_linear_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i32, c_i32, c_i32]),
     "mi355x_sample": (c_char_p, [c_void_p, c_i64, c_i64, c_i64, c_int, c_void_p, c_void_p,
                                  c_void_p, c_u64, c_u64, c_void_p, c_void_p]),

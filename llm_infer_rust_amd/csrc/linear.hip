@@ -225,6 +225,100 @@ __global__ __launch_bounds__(256) void linear_reduce(const float* __restrict__ p
   }
 }
 
+// Fused epilogue for a projection followed by the residual RMSNorm (o_proj and down of a
+// decoder layer): y = round(sum of the split-K partials) (or y read back rounded when K is
+// not split), residual <- round(y + residual), out <- round(rms(y + residual) * weight),
+// the norm on the unrounded fp32 sum. One 256-lane workgroup per row, 8 columns per chunk,
+// chunk c + 256 j per lane and the same two-level sum of squares as the stand-alone
+// residual RMSNorm for these widths, so the results equal the two separate passes bit for
+// bit.
+template <int DT, int NCH, bool PARTIAL>
+__global__ __launch_bounds__(256) void reduce_add_rms(const float* __restrict__ partial,
+                                                      int splits, uint16_t* out, int64_t ldo,
+                                                      uint16_t* residual, int64_t ldr,
+                                                      const uint16_t* __restrict__ weight,
+                                                      int M, int N, float eps) {
+  __shared__ float wave_ss[4];
+  const int64_t row = blockIdx.x;
+  const int chunks = N >> 3;
+  const int64_t plane = static_cast<int64_t>(M) * N;
+  float vals[NCH][8];
+  uint4 wraw[NCH];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int chunk = threadIdx.x + c * 256;
+    if (chunk < chunks) wraw[c] = ld128(weight + chunk * 8);
+  }
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int chunk = threadIdx.x + c * 256;
+    if (chunk >= chunks) continue;
+    if constexpr (PARTIAL) {
+      const float* p = partial + row * N + chunk * 8;
+      float4 lo = *reinterpret_cast<const float4*>(p);
+      float4 hi = *reinterpret_cast<const float4*>(p + 4);
+      for (int k = 1; k < splits; ++k) {
+        const float4 a = *reinterpret_cast<const float4*>(p + k * plane);
+        const float4 b = *reinterpret_cast<const float4*>(p + k * plane + 4);
+        lo.x += a.x;
+        lo.y += a.y;
+        lo.z += a.z;
+        lo.w += a.w;
+        hi.x += b.x;
+        hi.y += b.y;
+        hi.z += b.z;
+        hi.w += b.w;
+      }
+      const float y[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      unpack8<DT>(pack8<DT>(y), vals[c]);  // the projection's output, rounded once
+    } else {
+      unpack8<DT>(ld128(out + row * ldo + chunk * 8), vals[c]);
+    }
+    float r[8];
+    unpack8<DT>(ld128(residual + row * ldr + chunk * 8), r);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vals[c][i] += r[i];
+    st128(residual + row * ldr + chunk * 8, pack8<DT>(vals[c]));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = fmaf(vals[c][i], vals[c][i], ss);
+  }
+  ss = wave_sum(ss);
+  if (threadIdx.x % kWave == 0) wave_ss[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  ss = (wave_ss[0] + wave_ss[1]) + (wave_ss[2] + wave_ss[3]);
+  const float scale = rsqrtf(ss / static_cast<float>(N) + eps);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int chunk = threadIdx.x + c * 256;
+    if (chunk < chunks) {
+      float wf[8];
+      unpack8<DT>(wraw[c], wf);
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = (vals[c][i] * scale) * wf[i];
+      st128(out + row * ldo + chunk * 8, pack8<DT>(y));
+    }
+  }
+}
+
+template <int DT, bool PARTIAL>
+void launch_reduce_add_rms(const float* partial, int splits, uint16_t* out, int64_t ldo,
+                           uint16_t* residual, int64_t ldr, const uint16_t* weight, int M, int N,
+                           float eps, hipStream_t s) {
+  const int chunks = N / 8;
+  const dim3 grid(static_cast<uint32_t>(M)), block(256);
+  if (chunks <= 256)
+    reduce_add_rms<DT, 1, PARTIAL><<<grid, block, 0, s>>>(partial, splits, out, ldo, residual,
+                                                           ldr, weight, M, N, eps);
+  else if (chunks <= 512)
+    reduce_add_rms<DT, 2, PARTIAL><<<grid, block, 0, s>>>(partial, splits, out, ldo, residual,
+                                                           ldr, weight, M, N, eps);
+  else
+    reduce_add_rms<DT, 4, PARTIAL><<<grid, block, 0, s>>>(partial, splits, out, ldo, residual,
+                                                           ldr, weight, M, N, eps);
+}
+
 struct TileConfig {
   int bm, bn, wm, wn, stages;
 };
@@ -311,11 +405,14 @@ extern "C" int64_t mi355x_linear_workspace_bytes(int64_t M, int64_t N, int64_t K
   return c.splits > 1 ? int64_t(c.splits) * M * N * 4 : 0;
 }
 
-extern "C" const char* mi355x_linear(const void* x, int64_t ldx, const void* w, int64_t ldw,
-                                     void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
-                                     void* workspace, int64_t workspace_bytes, int32_t cus,
-                                     int32_t config, int32_t splits, int64_t dtype,
-                                     void* stream) {
+namespace mi355x {
+namespace {
+// Validates, picks the tiling and launches the projection. With `fuse_out_partials` the
+// split-K partials are left in the workspace (no reduce) and `*splits_used` tells how many.
+const char* run_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, void* out,
+                       int64_t ldo, int64_t M, int64_t N, int64_t K, void* workspace,
+                       int64_t workspace_bytes, int32_t cus, int32_t config, int32_t splits,
+                       int64_t dtype, bool leave_partials, int* splits_used, hipStream_t s) {
   if (!x || !w || !out) return set_error("mi355x_linear: null pointer");
   if (M <= 0 || N <= 0 || K <= 0 || M > 4096 || N % 4 || K % kBK || ldx < K || ldw < K ||
       ldo < N || ldx % 8 || ldw % 8 || ldo % 4 || (dtype != 0 && dtype != 1))
@@ -348,13 +445,13 @@ extern "C" const char* mi355x_linear(const void* x, int64_t ldx, const void* w, 
   a.groups = static_cast<int32_t>(ceil_div(int64_t(a.tiles_n) * a.splits, 8) * 8);
   const int64_t blocks = int64_t(a.groups) * a.tiles_m;
   if (blocks > (int64_t(1) << 31) - 1) return set_error("mi355x_linear: grid too large");
-  auto s = static_cast<hipStream_t>(stream);
   if (dtype == 0)
     launch_dt<0>(c.config, a, static_cast<int>(blocks), s);
   else
     launch_dt<1>(c.config, a, static_cast<int>(blocks), s);
   if (const char* e = launch_status("linear_kernel")) return e;
-  if (c.splits > 1) {
+  if (splits_used) *splits_used = c.splits;
+  if (c.splits > 1 && !leave_partials) {
     const int64_t quads = M * (N / 4);
     const int grid = static_cast<int>(std::min<int64_t>(ceil_div(quads, 256), 4096));
     if (dtype == 0)
@@ -364,4 +461,50 @@ extern "C" const char* mi355x_linear(const void* x, int64_t ldx, const void* w, 
     if (const char* e = launch_status("linear_reduce")) return e;
   }
   return nullptr;
+}
+}  // namespace
+}  // namespace mi355x
+
+extern "C" const char* mi355x_linear(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                     void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                                     void* workspace, int64_t workspace_bytes, int32_t cus,
+                                     int32_t config, int32_t splits, int64_t dtype,
+                                     void* stream) {
+  return run_linear(x, ldx, w, ldw, out, ldo, M, N, K, workspace, workspace_bytes, cus, config,
+                    splits, dtype, false, nullptr, static_cast<hipStream_t>(stream));
+}
+
+extern "C" const char* mi355x_linear_add_rms_norm(const void* x, int64_t ldx, const void* w,
+                                                  int64_t ldw, void* residual, int64_t ldr,
+                                                  const void* norm_weight, double eps, void* out,
+                                                  int64_t ldo, int64_t M, int64_t N, int64_t K,
+                                                  void* workspace, int64_t workspace_bytes,
+                                                  int32_t cus, int64_t dtype, void* stream) {
+  if (!residual || !norm_weight) return set_error("mi355x_linear_add_rms_norm: null pointer");
+  if (N % 8 || N / 8 <= 128 || N / 8 > 1024 || ldr % 8 || ldo % 8 || !aligned(residual, 16) ||
+      !aligned(out, 16) || !aligned(norm_weight, 16))
+    return set_error("mi355x_linear_add_rms_norm: width must be 1032..8192 in 16-byte rows");
+  auto s = static_cast<hipStream_t>(stream);
+  int used = 1;
+  if (const char* e = run_linear(x, ldx, w, ldw, out, ldo, M, N, K, workspace, workspace_bytes,
+                                 cus, -1, -1, dtype, true, &used, s))
+    return e;
+  const float* partial = static_cast<const float*>(workspace);
+  auto* o = static_cast<uint16_t*>(out);
+  auto* r = static_cast<uint16_t*>(residual);
+  const auto* g = static_cast<const uint16_t*>(norm_weight);
+  const int m = static_cast<int>(M), n = static_cast<int>(N);
+  const float fe = static_cast<float>(eps);
+  if (dtype == 0) {
+    if (used > 1)
+      launch_reduce_add_rms<0, true>(partial, used, o, ldo, r, ldr, g, m, n, fe, s);
+    else
+      launch_reduce_add_rms<0, false>(partial, 1, o, ldo, r, ldr, g, m, n, fe, s);
+  } else {
+    if (used > 1)
+      launch_reduce_add_rms<1, true>(partial, used, o, ldo, r, ldr, g, m, n, fe, s);
+    else
+      launch_reduce_add_rms<1, false>(partial, 1, o, ldo, r, ldr, g, m, n, fe, s);
+  }
+  return launch_status("reduce_add_rms");
 }

@@ -176,13 +176,10 @@ class Qwen3Model:
         hq, hkv, d = cfg.num_attention_heads, cfg.num_kv_heads, cfg.head_dim
         eps = cfg.rms_norm_eps
         hidden = F.embedding(input_ids, self.embed_tokens)
-        residual = None
-        for layer in self.layers:
-            if residual is None:
-                residual = hidden
-                x = ops.rms_norm(hidden, layer.input_layernorm, eps)
-            else:
-                x, residual = ops.add_rms_norm(hidden, residual, layer.input_layernorm, eps)
+        residual = hidden
+        x = ops.rms_norm(hidden, self.layers[0].input_layernorm, eps)
+        n_layers = len(self.layers)
+        for i, layer in enumerate(self.layers):
             qkv = ops.linear(x, layer.qkv_proj)
             q = qkv[:, : hq * d].view(t, hq, d)
             k = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
@@ -190,11 +187,15 @@ class Qwen3Model:
             ops.qk_norm_rope_store(q, k, v, layer.q_norm, layer.k_norm, eps, positions,
                                    self.rope, layer.base_attention, write_loc)
             attn = attention_batch.forward(q, k, v, layer.base_attention)
-            o = ops.linear(attn, layer.o_proj)
-            x, residual = ops.add_rms_norm(o, residual, layer.post_attention_layernorm, eps)
+            # o_proj + post-attention norm, down + the next layer's input norm (the final
+            # norm after the last layer): each a projection fused with its residual RMSNorm.
+            x, residual = ops.linear_add_rms_norm(attn, layer.o_proj, residual,
+                                                  layer.post_attention_layernorm, eps)
             gate_up = ops.linear(x, layer.gate_up_proj)
-            hidden = ops.linear(ops.silu_and_mul(gate_up), layer.down_proj)
-        hidden, _ = ops.add_rms_norm(hidden, residual, self.norm, eps)
+            next_norm = self.layers[i + 1].input_layernorm if i + 1 < n_layers else self.norm
+            x, residual = ops.linear_add_rms_norm(ops.silu_and_mul(gate_up), layer.down_proj,
+                                                  residual, next_norm, eps)
+        hidden = x
         if logits_indices is not None:
             hidden = hidden.index_select(0, logits_indices)
         if logits_out is not None:

@@ -263,6 +263,37 @@ def decode_linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | Non
     return out
 
 
+def linear_add_rms_norm(x: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
+                        norm_weight: torch.Tensor,
+                        eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """``y = linear(x, weight)`` then ``add_rms_norm(y, residual, norm_weight, eps)``,
+    returning ``(normed, residual)`` with ``residual`` updated in place. Decode-sized
+    products run as one projection plus one fused reduce/residual/norm pass (bit-identical
+    to the two separate steps); everything else runs the two steps."""
+    m, k = (x.shape if x.dim() == 2 else (0, 0))
+    n = weight.size(0)
+    if (x.is_cuda and x.dim() == 2 and x.stride(1) == 1 and weight.is_contiguous()
+            and uses_decode_kernel(m, n, k) and n % 8 == 0 and 128 < n // 8 <= 1024
+            and residual.dim() == 2 and residual.shape == (m, n) and residual.stride(1) == 1
+            and residual.dtype == x.dtype and residual.stride(0) % 8 == 0):
+        _require_device(x, "linear_add_rms_norm")
+        dt = dtype_code(x)
+        _check_weight(x, norm_weight, n)
+        if weight.dtype != x.dtype or weight.device != x.device or weight.size(1) != k:
+            raise NativeError("invalid linear operands: expected x [M, K] and weight [N, K]")
+        out = torch.empty((m, n), dtype=x.dtype, device=x.device)
+        cus = _native.device_cus(x.device)
+        need = lib().mi355x_linear_workspace_bytes(m, n, k, cus, -1, -1)
+        ws = torch.empty(max(int(need), 16), dtype=torch.uint8, device=x.device) if need else None
+        check(lib().mi355x_linear_add_rms_norm(
+            x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), residual.data_ptr(),
+            residual.stride(0), norm_weight.data_ptr(), float(eps), out.data_ptr(), n, m, n, k,
+            None if ws is None else ws.data_ptr(), int(need), cus, dt, stream_of(x)),
+            "linear_add_rms_norm")
+        return out, residual
+    return add_rms_norm(linear(x, weight), residual, norm_weight, eps)
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """``x @ weight.T``: decode-sized products on the gfx950 kernel, the rest on
     hipBLASLt (``src/layers/linear.rs:5-7``)."""
@@ -273,5 +304,6 @@ def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
 
 
 __all__ = ["rms_norm", "add_rms_norm", "qk_norm", "silu_and_mul", "HalfSplitRope", "rope",
-           "qk_norm_rope_store", "decode_linear", "linear", "uses_decode_kernel", "NativeError",
+           "qk_norm_rope_store", "decode_linear", "linear", "linear_add_rms_norm",
+           "uses_decode_kernel", "NativeError",
            "_native"]

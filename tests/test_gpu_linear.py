@@ -128,3 +128,34 @@ def test_graph_replays_match_eager(gpu):
         _ = ops.decode_linear(x, w * 0.5)  # eager work reusing the allocator between replays
         torch.cuda.synchronize()
 
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 4096, 4096), (256, 4096, 12288), (100, 2048, 1024),
+                                   (1, 4096, 4096), (64, 2048, 64)])
+def test_fused_residual_norm_equals_separate_passes(gpu, m, n, k):
+    """mi355x_linear_add_rms_norm == decode_linear then add_rms_norm, bit for bit, for split
+    (fp32 partials reduced in the norm pass) and unsplit (K = 64) projections."""
+    x, w = operands(m, n, k, torch.bfloat16, gpu, m * 7 + n + k)
+    g = torch.Generator().manual_seed(n + k)
+    residual = torch.randn(m, n, generator=g).to(torch.bfloat16).to(gpu)
+    gamma = (torch.rand(n, generator=g) + 0.5).to(torch.bfloat16).to(gpu)
+    res_sep = residual.clone()
+    y = ops.decode_linear(x, w)
+    want, _ = ops.add_rms_norm(y, res_sep, gamma, 1e-6)
+    res_fused = residual.clone()
+    got, res_out = ops.linear_add_rms_norm(x, w, res_fused, gamma, 1e-6)
+    assert res_out.data_ptr() == res_fused.data_ptr()
+    assert torch.equal(res_fused, res_sep)
+    assert torch.equal(got, want)
+
+
+def test_fused_residual_norm_falls_back_outside_decode_sizes(gpu):
+    """Prefill-sized rows (or widths the fused pass does not take) run the two steps."""
+    x, w = operands(300, 1024, 512, torch.bfloat16, gpu, 9)
+    g = torch.Generator().manual_seed(9)
+    residual = torch.randn(300, 1024, generator=g).to(torch.bfloat16).to(gpu)
+    gamma = (torch.rand(1024, generator=g) + 0.5).to(torch.bfloat16).to(gpu)
+    res_a, res_b = residual.clone(), residual.clone()
+    got, _ = ops.linear_add_rms_norm(x, w, res_a, gamma, 1e-6)
+    want, _ = ops.add_rms_norm(F.linear(x, w), res_b, gamma, 1e-6)
+    assert torch.equal(got, want) and torch.equal(res_a, res_b)
