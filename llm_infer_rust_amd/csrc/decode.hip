@@ -694,6 +694,215 @@ __global__ __launch_bounds__(64 * W, 1) void decode_dma_kernel(DecodeArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// decode_mma_kernel: decode_dma_kernel's copy pipeline with the math on the matrix
+// cores, for GQA groups of 4..16 q heads per kv head (Qwen3-8B: 4). Per 16-token tile,
+// wave w (kv head w of the slice) computes
+//   S = K Q^T   with v_mfma_f32_16x16x32 (A = 16 K rows, B = the group's q heads as
+//               columns; columns past the group are zero), 4 MFMAs over d = 128;
+//   P = 2^(S scale - m) per column (online softmax; the S accumulator already holds each
+//               lane's 4 tokens of one column, the B layout of the next product);
+//   O^T += V^T P^T with v_mfma_f32_16x16x16, 8 MFMAs (one per 16 dims), the V^T operand
+//               read transposed from the row-major V tile with ds_read_b64_tr_b16.
+// The copies place 16-byte chunk c of a head's 256 bytes at position c ^ (token & 15) of
+// its token row, so the 16 rows an MFMA operand read touches land in distinct banks.
+// ---------------------------------------------------------------------------
+typedef __bf16 mma_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 mma_bf16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 mma_f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 mma_f16x4_t __attribute__((ext_vector_type(4)));
+typedef float mma_floatx4 __attribute__((ext_vector_type(4)));
+typedef short mma_v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) mma_v4i16_t mma_lds_v4i16;
+
+template <int DT>
+__device__ __forceinline__ mma_floatx4 mma_16x16x32(const uint4& a, const uint4& b,
+                                                    mma_floatx4 c) {
+  if constexpr (DT == 0)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mma_bf16x8_t, a),
+                                                   __builtin_bit_cast(mma_bf16x8_t, b), c, 0, 0,
+                                                   0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mma_f16x8_t, a),
+                                                  __builtin_bit_cast(mma_f16x8_t, b), c, 0, 0, 0);
+}
+
+template <int DT>
+__device__ __forceinline__ mma_floatx4 mma_16x16x16(const uint2& a, const uint2& b,
+                                                    mma_floatx4 c) {
+  if constexpr (DT == 0)
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(mma_v4i16_t, a),
+                                                     __builtin_bit_cast(mma_v4i16_t, b), c, 0,
+                                                     0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(mma_f16x4_t, a),
+                                                 __builtin_bit_cast(mma_f16x4_t, b), c, 0, 0, 0);
+}
+
+template <int DT, int G, int W, int S>
+__global__ __launch_bounds__(64 * W, 1) void decode_mma_kernel(DecodeArgs a) {
+  constexpr int T = 16;                         // tokens per tile = the MFMAs' 16 rows
+  constexpr int kRow = W * 256;                 // bytes of one token's slice (K or V)
+  constexpr int kHalf = T * kRow;               // K (or V) bytes of one tile
+  constexpr int kStage = 2 * kHalf;
+  constexpr int kCopies = 2 * kHalf / 1024;     // 1 KiB copies per tile
+  constexpr int kPerWave = kCopies / W;
+  static_assert(G >= 2 && G <= 16, "the q heads of a group are the MFMA columns");
+  static_assert(kRow >= 1024 && kRow % 1024 == 0 && kCopies % W == 0, "tile shape");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[S * kStage];
+  __shared__ int32_t entries[kDmaMaxEntries];
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;   // MFMA column (q head of the group) / operand row
+  const int quad = lane >> 4;  // 16-lane group
+  const int h = blockIdx.y * W + wave;  // kv head
+  const int wg = blockIdx.x;
+  if (wg >= a.ints[0]) return;  // graph plans launch a fixed capacity
+  if (a.num_kv_heads < 0) lds[threadIdx.x] = 0;  // the copies are invisible to the compiler
+  const uint32_t lds_base = lds_address(lds);
+  const uint32_t row_elems = static_cast<uint32_t>(a.num_kv_heads) * kHeadDim;
+  const uint16_t* kslice = a.k_cache + blockIdx.y * W * kHeadDim;
+  const uint16_t* vslice = a.v_cache + blockIdx.y * W * kHeadDim;
+  const int item_end = a.ints[a.o_wg + wg + 1];
+
+  // Read offsets within a stage for this wave's head (token-independent parts).
+  const int head_off = wave * 256;
+
+  for (int item = a.ints[a.o_wg + wg]; item < item_end; ++item) {
+    const int4 wi = reinterpret_cast<const int4*>(a.ints + a.o_work)[item];
+    const int req = wi.x, beg = wi.y, end = wi.z, pslot = wi.w;
+    const int first_page = beg / a.page_size;
+    const int n_entries = (end - 1) / a.page_size - first_page + 1;
+    const int32_t* pages = a.indices + a.ints[a.o_indptr + req] + first_page;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n_entries; i += blockDim.x) entries[i] = pages[i];
+    // Q^T as the B operand: lane holds q head (h G + col) dims 32 kk + 8 quad .. + 8;
+    // columns past the group are zero.
+    uint4 qb[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      qb[kk] = col < G ? ld128(a.q + req * a.q_stride_n + (h * G + col) * a.q_stride_h +
+                               32 * kk + 8 * quad)
+                       : make_uint4(0, 0, 0, 0);
+    }
+    wait_vmem_loads();
+    __syncthreads();
+
+    const int n_tiles = (end - beg + T - 1) / T;
+    // Copy c of a tile: half c / (kCopies / 2) (K, V), token (c % (kCopies / 2)) * 1024 /
+    // kRow of the tile, byte (c * 1024) % kRow of its row; the token is wave-uniform.
+    // Lane i fetches the chunk that belongs at position i: chunk (i ^ (token & 15)) of
+    // the same head.
+    auto issue = [&](int t, int stage) {
+#pragma unroll
+      for (int j = 0; j < kPerWave; ++j) {
+        const int c = wave * kPerWave + j;
+        const int half = c / (kCopies / 2);
+        const int r = c % (kCopies / 2);
+        const int tile_tok = (r * 1024) / kRow;
+        const int tok = min(beg + t * T + tile_tok, end - 1);
+        const int e = entries[tok / a.page_size - first_page];
+        const uint32_t slot = static_cast<uint32_t>(e) * static_cast<uint32_t>(a.page_size) +
+                              static_cast<uint32_t>(tok % a.page_size);
+        const int chunk = ((r * 1024) % kRow) / 16 + lane;  // position within the row
+        const int src_chunk = (chunk & ~15) | ((chunk & 15) ^ (tile_tok & 15));
+        const uint16_t* src =
+            (half ? vslice : kslice) + static_cast<uint64_t>(slot) * row_elems + src_chunk * 8;
+        copy_to_lds(src, lds_base + stage * kStage + half * kHalf + r * 1024);
+      }
+    };
+
+    mma_floatx4 o[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) o[b] = mma_floatx4{0.f, 0.f, 0.f, 0.f};
+    float m = -1e30f, l = 0.f;  // of column `col`; m is the same in the 4 lane groups
+
+#pragma unroll
+    for (int st = 0; st < S - 1; ++st)
+      if (st < n_tiles) issue(st, st);
+    for (int t = 0; t < n_tiles; ++t) {
+      wait_tiles_ahead<kPerWave, S - 2>(min(S - 2, n_tiles - 1 - t));
+      __syncthreads();
+      if (t + S - 1 < n_tiles) issue(t + S - 1, (t + S - 1) % S);
+      const uint8_t* kb = lds + (t % S) * kStage + head_off;
+      const uint8_t* vb = kb + kHalf;
+      // S = K Q^T: lane reads token `col`, chunk 4 kk + quad (swizzled).
+      mma_floatx4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(kb + col * kRow +
+                                                          (((4 * kk + quad) ^ col) * 16));
+        sc = mma_16x16x32<DT>(kf, qb[kk], sc);
+      }
+      // V^T operands (transposed reads): block b, lane p of group quad addresses token
+      // 4 quad + p / 4, dims 16 b + 4 (p % 4) .. + 3.
+      uint2 vf[8];
+      {
+        const int vt = 4 * quad + (col >> 2);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+          const int chunk = 2 * b + ((col & 3) >> 1);
+          lds_u8* vp = (lds_u8*)vb + vt * kRow + ((chunk ^ vt) * 16) + 8 * (col & 1);
+          vf[b] = __builtin_bit_cast(
+              uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((mma_lds_v4i16*)vp));
+        }
+      }
+      // Lane holds S[token 4 quad + i][col]; tokens past the item are masked.
+      float s[4];
+      float mx = m;
+      const int tok0 = beg + t * T + 4 * quad;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[i] = tok0 + i < end ? sc[i] * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, s[i]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float corr = __builtin_amdgcn_exp2f(m - mx);
+      m = mx;
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(s[i] - mx);
+      l = l * corr + ((p[0] + p[1]) + (p[2] + p[3]));
+      const uint2 pb = make_uint2(Elem<DT>::pack2(p[0], p[1]), Elem<DT>::pack2(p[2], p[3]));
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[b][i] *= corr;
+        o[b] = mma_16x16x16<DT>(vf[b], pb, o[b]);
+      }
+    }
+
+    // Column totals: l summed over the 4 lane groups (m is already common).
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (col < G) {
+      const int qh = h * G + col;
+      const float inv = 1.f / l;
+      // Lane holds O^T[16 b + 4 quad + i][col].
+      if (pslot < 0) {
+        uint16_t* dst = a.out + req * a.out_stride_n + qh * a.out_stride_h + 4 * quad;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+          *reinterpret_cast<uint2*>(dst + 16 * b) =
+              make_uint2(Elem<DT>::pack2(o[b][0] * inv, o[b][1] * inv),
+                         Elem<DT>::pack2(o[b][2] * inv, o[b][3] * inv));
+      } else {
+        float* dst = a.partial_o +
+                     (static_cast<int64_t>(pslot) * a.num_q_heads + qh) * kHeadDim + 4 * quad;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+          *reinterpret_cast<float4*>(dst + 16 * b) =
+              make_float4(o[b][0] * inv, o[b][1] * inv, o[b][2] * inv, o[b][3] * inv);
+        if (quad == 0)
+          a.partial_lse[static_cast<int64_t>(pslot) * a.num_q_heads + qh] =
+              m + __builtin_amdgcn_logf(l);
+      }
+    }
+  }
+}
+
 // Split-KV merge: one wave per (request, q head), two dims per lane. Chunks are
 // combined with a running log2-sum-exp; the chunk loop is unrolled so the
 // partial loads of several chunks are in flight together.
@@ -780,8 +989,27 @@ bool dispatch_group(const DecodeArgs& a, int group, dim3 grid, int waves, bool p
   }
 }
 
+// Matrix-core math for GQA groups of 4 or more (MI355X_DECODE_MMA=0 turns it off; tuning
+// knob, read once).
+bool mma_enabled() {
+  static const bool on = [] {
+    const char* env = std::getenv("MI355X_DECODE_MMA");
+    return !(env && std::strcmp(env, "0") == 0);
+  }();
+  return on;
+}
+
 template <int DT, int G>
 void launch_dma(const DecodeArgs& a, dim3 grid, int waves, hipStream_t s) {
+  if constexpr (G >= 4) {
+    if (mma_enabled()) {
+      if (waves == 8)
+        decode_mma_kernel<DT, G, 8, kDmaStages><<<grid, dim3(8 * kWave), 0, s>>>(a);
+      else
+        decode_mma_kernel<DT, G, 4, kDmaStages><<<grid, dim3(4 * kWave), 0, s>>>(a);
+      return;
+    }
+  }
   if (waves == 8)
     decode_dma_kernel<DT, G, 8, kDmaTile, kDmaStages><<<grid, dim3(8 * kWave), 0, s>>>(a);
   else

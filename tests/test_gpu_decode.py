@@ -139,7 +139,9 @@ def _random_decode_case(gpu, g, rng, b, hq, hkv, page_size, lo, hi, pool_pages, 
     (16, 8, 1, torch.bfloat16), (32, 8, 16, torch.bfloat16), (8, 8, 4, torch.bfloat16),
     (64, 8, 1, torch.bfloat16), (16, 8, 1, torch.float16), (4, 2, 3, torch.float16),
     # slices of 4 kv heads, two slices of 8, page sizes that do not divide the 16-token tile
-    (16, 4, 3, torch.bfloat16), (32, 16, 7, torch.bfloat16), (8, 4, 16, torch.float16)])
+    (16, 4, 3, torch.bfloat16), (32, 16, 7, torch.bfloat16), (8, 4, 16, torch.float16),
+    # groups of 4 and 8 q heads run the matrix-core kernel: fp16, odd pages, 4-head slices
+    (32, 8, 5, torch.float16), (64, 8, 16, torch.bfloat16), (32, 4, 1, torch.bfloat16)])
 def test_decode_matches_oracle(gpu, hq, hkv, page_size, dtype):
     g = torch.Generator().manual_seed(hq * 7 + page_size)
     rng = np.random.default_rng(hq + page_size)
@@ -164,9 +166,11 @@ def test_decode_matches_oracle(gpu, hq, hkv, page_size, dtype):
     assert bool((storage[len(lens):] == 99.0).all())
 
 
-def test_long_and_tiny_requests_split_across_workgroups(gpu):
+@pytest.mark.parametrize("hq", [16, 32])
+def test_long_and_tiny_requests_split_across_workgroups(gpu, hq):
     """Requests far longer than one workgroup's share (and than one work item) next to
-    requests of a few tokens: every share boundary and item cut is merged exactly."""
+    requests of a few tokens: every share boundary and item cut is merged exactly (group 2
+    on the vector kernel, group 4 on the matrix-core kernel)."""
     g = torch.Generator().manual_seed(99)
     page = 2
     lens = np.array([20011, 5, 9000, 1, 2048, 4097], dtype=np.int32)
@@ -181,8 +185,8 @@ def test_long_and_tiny_requests_split_across_workgroups(gpu):
         off += n
     kc = randn((pool_pages, page, 8, 128), g, torch.bfloat16, gpu)
     vc = randn((pool_pages, page, 8, 128), g, torch.bfloat16, gpu)
-    q = randn((len(lens), 16, 128), g, torch.bfloat16, gpu)
-    attn = make_backend(gpu, 16, 8, page)
+    q = randn((len(lens), hq, 128), g, torch.bfloat16, gpu)
+    attn = make_backend(gpu, hq, 8, page)
     cache = BaseAttention()
     cache.bind_kv_cache(kc, vc)
     meta = AttentionMetadata(BatchPhase.DECODE, block_table=torch.from_numpy(table).to(gpu),
@@ -192,7 +196,7 @@ def test_long_and_tiny_requests_split_across_workgroups(gpu):
     oplan.check_work_list(md["work"], md["merge"], lens.tolist())
     out = batch.forward(q, q, q, cache)
     want = oatt.decode_with_cache(f32(q), f32(kc), f32(vc), table, lens, page)
-    assert_close(f32(out).reshape(want.shape), want, "long/tiny")
+    assert_close(f32(out).reshape(want.shape), want, f"long/tiny hq={hq}")
 
 
 def test_config2_shape_parity(gpu):
