@@ -205,7 +205,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
   // group's first (clamped) key; their ids are read with one uniform load from the
   // constant address space (the words are read-only here), which becomes a scalar load
   // counted on lgkmcnt and so never waits on the tile copies counted by vmcnt.
-  auto issue = [&](int t, int stage) {
+  auto issue_general = [&](int t, int stage) {
     const uint32_t sbase = lds_base + stage * kStageBytes;
 #pragma unroll
     for (int j = 0; j < kGroupsPerWave; ++j) {
@@ -234,6 +234,51 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
       copy_to_lds(k_req + slot * a.k_sn + kc * 8, sbase + g * 1024);
       copy_to_lds(v_req + slot * a.v_sn + vc * 8, sbase + kTileBytes + g * 1024);
     }
+  };
+
+  // Every tile but an item's last lies wholly inside the keys, so no clamping is needed
+  // and the per-lane part of each copy address is fixed for the whole loop: row r of
+  // tile t sits at lane_k + (key or slot of its group's first row) * stride. Ragged
+  // mode: key t * 64 + 4 g. Paged mode with a page size of 4..64 that divides 64 (the
+  // serving sizes): the 4 rows of a group lie in one page, so the group needs one
+  // page id (page t * 64 / P + 4 g / P of the request) and one uniform multiply.
+  const bool fast_pages = !PAGED || (a.page_size >= 4 && a.page_size <= kTileK &&
+                                     kTileK % a.page_size == 0);
+  const uint16_t* lane_k[kGroupsPerWave];
+  const uint16_t* lane_v[kGroupsPerWave];
+#pragma unroll
+  for (int j = 0; j < kGroupsPerWave; ++j) {
+    const int g = wave * kGroupsPerWave + j;
+    const int row = 4 * g + row_in_group;
+    const int kc = pos ^ (row & 15);
+    const int vc = pos ^ (4 * (row & 3));
+    lane_k[j] = k_req + static_cast<int64_t>(row_in_group) * a.k_sn + kc * 8;
+    lane_v[j] = v_req + static_cast<int64_t>(row_in_group) * a.v_sn + vc * 8;
+  }
+  const int pages_per_tile = PAGED && fast_pages ? kTileK / a.page_size : 0;
+  auto issue_fast = [&](int t, int stage) {
+    const uint32_t sbase = lds_base + stage * kStageBytes;
+#pragma unroll
+    for (int j = 0; j < kGroupsPerWave; ++j) {
+      const int g = wave * kGroupsPerWave + j;
+      int64_t first;  // key (ragged) or slot (paged) of the group's first row
+      if constexpr (PAGED) {
+        const int p = t * pages_per_tile + (4 * g) / a.page_size;
+        const int page =
+            *((const __attribute__((address_space(4))) int32_t*)(a.indices) + rq.page_base + p);
+        first = static_cast<int64_t>(page) * a.page_size + (4 * g) % a.page_size;
+      } else {
+        first = t * kTileK + 4 * g;
+      }
+      copy_to_lds(lane_k[j] + first * a.k_sn, sbase + g * 1024);
+      copy_to_lds(lane_v[j] + first * a.v_sn, sbase + kTileBytes + g * 1024);
+    }
+  };
+  auto issue = [&](int t, int stage) {
+    if (fast_pages && t + 1 < n_tiles)
+      issue_fast(t, stage);
+    else
+      issue_general(t, stage);
   };
 
   // Read side offsets (bytes within a stage).
