@@ -92,3 +92,33 @@ def test_linear_workspace_bytes_query(native):
     assert f(0, 4096, 4096, 256, -1, -1) == -1
     # the library's own choice for the Qwen3-8B down projection splits K
     assert f(256, 4096, 12288, 256, -1, -1) > 0
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_prefill_schedule_covers_every_query_block_once(native, seed):
+    """mi355x_prefill_schedule: every (request, 32 x 8 / heads-per-block query block, kv
+    head, head group) appears exactly once, and items come longest causal horizon first."""
+    rng = np.random.default_rng(seed)
+    b = int(rng.integers(1, 12))
+    hq, hkv = [(16, 8), (32, 8), (8, 8), (64, 8), (8, 1)][seed]
+    q_lens = rng.integers(1, 900, size=b)
+    prefixes = rng.integers(0, 3000, size=b) * (rng.random(b) < 0.5)
+    q_host = (ctypes.c_int32 * (b + 1))(*([0] + np.cumsum(q_lens).tolist()))
+    p_host = (ctypes.c_int32 * b)(*prefixes.tolist())
+    lib = native.lib()
+    n = lib.mi355x_prefill_schedule(q_host, p_host, b, hq, hkv, None, 0)
+    work = (ctypes.c_int32 * (4 * n))()
+    assert lib.mi355x_prefill_schedule(q_host, p_host, b, hq, hkv, work, n) == n
+    items = np.array(list(work), dtype=np.int64).reshape(n, 4)
+    group = hq // hkv
+    hpb = min(group, 8)
+    bq = 32 * (8 // hpb)
+    want = {(r, q0, h, g) for r in range(b) for q0 in range(0, int(q_lens[r]), bq)
+            for h in range(hkv) for g in range(group // hpb)}
+    got = [tuple(int(v) for v in row) for row in items]
+    assert len(got) == len(set(got)) and set(got) == want
+    horizon = [int(prefixes[r]) + min(q0 + bq, int(q_lens[r])) for r, q0, _, _ in got]
+    tiles = [(h + 63) // 64 for h in horizon]
+    assert tiles == sorted(tiles, reverse=True)
+    # a capacity below the item count is refused
+    assert lib.mi355x_prefill_schedule(q_host, p_host, b, hq, hkv, work, n - 1) == -1
