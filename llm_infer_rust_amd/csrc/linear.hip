@@ -481,9 +481,11 @@ extern "C" const char* mi355x_linear_add_rms_norm(const void* x, int64_t ldx, co
                                                   void* workspace, int64_t workspace_bytes,
                                                   int32_t cus, int64_t dtype, void* stream) {
   if (!residual || !norm_weight) return set_error("mi355x_linear_add_rms_norm: null pointer");
-  if (N % 8 || N / 8 <= 128 || N / 8 > 1024 || ldr % 8 || ldo % 8 || !aligned(residual, 16) ||
-      !aligned(out, 16) || !aligned(norm_weight, 16))
+  if (N % 8 || N / 8 <= 128 || N / 8 > 1024 || ldr < N || ldr % 8 || ldo % 8 ||
+      !aligned(residual, 16) || !aligned(out, 16) || !aligned(norm_weight, 16))
     return set_error("mi355x_linear_add_rms_norm: width must be 1032..8192 in 16-byte rows");
+  if (out == residual)  // the norm pass reads and writes both
+    return set_error("mi355x_linear_add_rms_norm: out and residual must not alias");
   auto s = static_cast<hipStream_t>(stream);
   int used = 1;
   if (const char* e = run_linear(x, ldx, w, ldw, out, ldo, M, N, K, workspace, workspace_bytes,

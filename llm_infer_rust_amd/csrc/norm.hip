@@ -277,6 +277,7 @@ extern "C" const char* mi355x_rms_norm(const void* x, const void* weight, void* 
                                        int dtype, void* stream) {
   if (tokens < 0 || heads <= 0 || width <= 0) return set_error("mi355x_rms_norm: bad shape");
   if (tokens == 0) return nullptr;
+  if (!x || !weight || !out) return set_error("mi355x_rms_norm: null pointer");
   NormArgs a{};
   a.x = const_cast<uint16_t*>(static_cast<const uint16_t*>(x));
   a.out = static_cast<uint16_t*>(out);
@@ -298,6 +299,7 @@ extern "C" const char* mi355x_add_rms_norm(void* x, void* residual, const void* 
                                            void* stream) {
   if (tokens < 0 || width <= 0) return set_error("mi355x_add_rms_norm: bad shape");
   if (tokens == 0) return nullptr;
+  if (!x || !residual || !weight) return set_error("mi355x_add_rms_norm: null pointer");
   if (x == residual) return set_error("mi355x_add_rms_norm: x and residual must not alias");
   NormArgs a{};
   a.x = static_cast<uint16_t*>(x);
@@ -324,6 +326,8 @@ extern "C" const char* mi355x_qk_norm(void* q, void* k, const void* q_weight,
   if (tokens < 0 || q_heads < 0 || k_heads < 0 || width <= 0)
     return set_error("mi355x_qk_norm: bad shape");
   if (tokens == 0 || q_heads + k_heads == 0) return nullptr;
+  if ((q_heads && (!q || !q_weight)) || (k_heads && (!k || !k_weight)))
+    return set_error("mi355x_qk_norm: null pointer");
   NormArgs a{};
   a.x = static_cast<uint16_t*>(q);
   a.residual = static_cast<uint16_t*>(k);

@@ -122,3 +122,48 @@ def test_prefill_schedule_covers_every_query_block_once(native, seed):
     assert tiles == sorted(tiles, reverse=True)
     # a capacity below the item count is refused
     assert lib.mi355x_prefill_schedule(q_host, p_host, b, hq, hkv, work, n - 1) == -1
+
+
+def test_entry_points_reject_bad_arguments_before_launching(native):
+    """Argument validation of the compute entries runs on the host and returns the error
+    string without touching the device (fake addresses are never dereferenced)."""
+    lib = native.lib()
+    a, b, c = 0x10000, 0x20000, 0x30000  # 16-byte aligned, never dereferenced
+
+    def err(r):
+        assert r is not None
+        return r.decode()
+
+    assert "null pointer" in err(lib.mi355x_rms_norm(None, None, None, 4, 1, 128, 128, 128,
+                                                      1e-6, 0, None))
+    assert "null pointer" in err(lib.mi355x_add_rms_norm(None, b, c, 4, 128, 128, 128, 1e-6,
+                                                          0, None))
+    assert "alias" in err(lib.mi355x_add_rms_norm(a, a, c, 4, 128, 128, 128, 1e-6, 0, None))
+    assert "null pointer" in err(lib.mi355x_qk_norm(a, None, b, c, 4, 2, 1, 128, 384, 128,
+                                                     384, 128, 1e-6, 0, None))
+    assert "bad shape" in err(lib.mi355x_rms_norm(a, b, c, -1, 1, 128, 128, 128, 1e-6, 0, None))
+    # zero tokens is a no-op, not an error
+    assert lib.mi355x_rms_norm(None, None, None, 0, 1, 128, 128, 128, 1e-6, 0, None) is None
+    assert "null pointer" in err(lib.mi355x_store_kv(a, b, None, c, a, 4, 8, 128, 100, 1024,
+                                                      128, 1024, 128, 0, False, None, None))
+    assert "invalid geometry" in err(lib.mi355x_store_kv(a, b, c, c, a, 4, 0, 128, 100, 1024,
+                                                          128, 1024, 128, 0, False, None, None))
+    # projections: K not a multiple of 64, too many rows, split-K without a workspace
+    assert "unsupported shape" in err(lib.mi355x_linear(a, 96, b, 96, c, 64, 8, 64, 96, None,
+                                                         0, 256, -1, -1, 0, None))
+    assert "unsupported shape" in err(lib.mi355x_linear(a, 128, b, 128, c, 64, 4097, 64, 128,
+                                                         None, 0, 256, -1, -1, 0, None))
+    assert "workspace" in err(lib.mi355x_linear(a, 1024, b, 1024, c, 256, 64, 256, 1024, None,
+                                                0, 256, 6, 4, 0, None))
+    assert "invalid tile" in err(lib.mi355x_linear(a, 1024, b, 1024, c, 256, 64, 256, 1024,
+                                                   None, 0, 256, 99, 1, 0, None))
+    # fused projection + residual norm: residual rows narrower than N, out aliasing residual
+    assert "width" in err(lib.mi355x_linear_add_rms_norm(a, 4096, b, 4096, c, 2048, a, 1e-6, b,
+                                                         4096, 8, 4096, 4096, None, 0, 256, 0,
+                                                         None))
+    assert "alias" in err(lib.mi355x_linear_add_rms_norm(a, 4096, b, 4096, c, 4096, a, 1e-6, c,
+                                                         4096, 8, 4096, 4096, None, 0, 256, 0,
+                                                         None))
+    assert "null pointer" in err(lib.mi355x_sample(None, 2, 100, 100, 0, None, None, None, 1, 0,
+                                                   None, None))
+    assert "bad shape" in err(lib.mi355x_silu_mul(a, b, -1, 64, 0, None))
