@@ -430,13 +430,6 @@ def main():
     from llm_infer_rust_amd.kv_cache import BaseAttention
 
     dev = torch.device("cuda", 0)
-    if args.only == "e2e":
-        print(json.dumps({"e2e": e2e_section(dev, args)}))
-        return
-    if args.only in ("prefill", "norms"):
-        fn = prefill_sections if args.only == "prefill" else norm_sections
-        print(json.dumps({args.only: fn(dev, max(args.steps, 20))}))
-        return
     if args.copy_calibration:
         src = torch.empty(COPY_CAL_BYTES // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
@@ -444,6 +437,13 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.only == "e2e":
+        print(json.dumps({"e2e": e2e_section(dev, args)}))
+        return
+    if args.only in ("prefill", "norms"):
+        fn = prefill_sections if args.only == "prefill" else norm_sections
+        print(json.dumps({args.only: fn(dev, max(args.steps, 20))}))
+        return
     w = build_workload(args.seed, dev)
     if args.only == "ceilings":
         print(json.dumps({"ceilings": ceilings_section(dev, w, max(min(args.steps, 50), 5))}))
