@@ -262,6 +262,7 @@ const char* mi355x_linear(const void* x, int64_t ldx, const void* w, int64_t ldw
  * split-K partials are reduced inside the norm pass instead of a separate
  * launch. Width N: a multiple of 8 in 1032..8192 (rows of 16-byte chunks);
  * library-chosen tiling, workspace as for mi355x_linear (config = splits = -1).
+ * ldr >= N; out and residual must not alias (the norm pass reads and writes both).
  * Replaces linear.rs:5-7 followed by ops.rs:22-35 (fused_ops.cu:300-338). */
 const char* mi355x_linear_add_rms_norm(const void* x, int64_t ldx, const void* w, int64_t ldw,
                                        void* residual, int64_t ldr, const void* norm_weight,
