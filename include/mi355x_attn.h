@@ -270,6 +270,20 @@ const char* mi355x_linear_add_rms_norm(const void* x, int64_t ldx, const void* w
                                        int64_t K, void* workspace, int64_t workspace_bytes,
                                        int32_t cus, int64_t dtype, void* stream);
 
+/* A gate_up projection fused with SiLU x mul (the MLP's first two steps):
+ *   y = x . w^T with w = [gate rows (width); up rows (width)] of [2 width, K],
+ *   out[m, j] = round(silu(g) * u), g = round(y[m, j]), u = round(y[m, width + j]),
+ * computed without writing y: equal bit for bit to mi355x_linear (unsplit, the
+ * same tiling) followed by mi355x_silu_mul. K is never split, so no workspace.
+ * config < 0 lets the library choose the tile shape by M (0, 6 and 7 are fused);
+ * cus is accepted for the same call shape as mi355x_linear.
+ * M <= 4096, K % 64 == 0, width % 4 == 0, 16-byte aligned x / w rows.
+ * Replaces linear.rs:5-7 (gate_up, mlp.rs) followed by ops.rs:53-61
+ * (fused_ops.cu:135-171). */
+const char* mi355x_linear_silu_mul(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                   void* out, int64_t ldo, int64_t M, int64_t width, int64_t K,
+                                   int32_t cus, int32_t config, int64_t dtype, void* stream);
+
 /* Workspace bytes mi355x_linear needs for this shape and tiling (0 when K is
  * not split, -1 for an invalid shape). Host-only. */
 int64_t mi355x_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t cus,

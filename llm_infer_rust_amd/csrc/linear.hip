@@ -66,8 +66,20 @@ struct LinearArgs {
 // distinct, so 32 lanes reading one chunk of 32 rows hit every bank evenly.
 __device__ __forceinline__ int chunk_pos(int c, int r) { return c ^ ((r & 7) ^ ((r >> 3) & 1)); }
 
-template <int DT, int BM, int BN, int WM, int WN, int STAGES, bool PARTIAL>
+// With SILU the product is a gate_up projection, w = [gate rows (N/2); up rows (N/2)], and
+// the kernel writes silu(gate) * up ([M, N/2]) instead of the product: rows 8 q .. 8 q + 7 of
+// each 32-row block of the weight tile come from gate for even q and from the matching up
+// rows for odd q, so every lane holds gate column j and up column j side by side (see the
+// epilogue) and the gate_up product never reaches memory.
+__device__ __forceinline__ int silu_tile_row(int n0, int r, int half_n, bool* up) {
+  const int rr = r & 31, q = rr >> 3;
+  *up = (q & 1) != 0;
+  return n0 / 2 + (r >> 5) * 16 + (q >> 1) * 8 + (rr & 7);  // output column
+}
+
+template <int DT, int BM, int BN, int WM, int WN, int STAGES, bool PARTIAL, bool SILU = false>
 __global__ __launch_bounds__(64 * WM * WN, 1) void linear_kernel(LinearArgs a) {
+  static_assert(!(SILU && PARTIAL), "the fused SiLU epilogue needs the whole K range");
   constexpr int NW = WM * WN;
   constexpr int kWaveM = BM / WM, kWaveN = BN / WN;  // wave tile
   constexpr int A_BLK = kWaveN / 32, B_BLK = kWaveM / 32;
@@ -112,7 +124,14 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void linear_kernel(LinearArgs a) {
       src[j] = a.x + static_cast<int64_t>(m) * a.ldx + k_begin + chunk_pos(pos, row) * 8;
     } else {
       const int r = row - BM;
-      const int n = min(n0 + r, a.N - 1);
+      int n;
+      if constexpr (SILU) {
+        bool up;
+        const int oc = min(silu_tile_row(n0, r, a.N / 2, &up), a.N / 2 - 1);
+        n = up ? a.N / 2 + oc : oc;
+      } else {
+        n = min(n0 + r, a.N - 1);
+      }
       src[j] = a.w + static_cast<int64_t>(n) * a.ldw + k_begin + chunk_pos(pos, r) * 8;
     }
     dst[j] = lds_base + g * 1024;
@@ -177,6 +196,33 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void linear_kernel(LinearArgs a) {
 
   // Lane holds D[n][m] for m = column `col` of each B block and n = 8 q + 4 half + e
   // (e = 0..3) of each A block, accumulator elements 4 q + e.
+  if constexpr (SILU) {
+    // Quads q (gate) and q + 1 (up) hold the same 4 output columns: round both as the
+    // stand-alone product would, then silu(g) * u exactly as the stand-alone SiLU pass.
+#pragma unroll
+    for (int j = 0; j < B_BLK; ++j) {
+      const int m = m0 + wm * kWaveM + 32 * j + col;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int i = 0; i < A_BLK; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; q += 2) {
+          bool up;
+          const int oc = silu_tile_row(n0, wn * kWaveN + 32 * i + 8 * q + 4 * half, a.N / 2, &up);
+          if (oc >= a.N / 2) continue;
+          float g[4], u[4], y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            g[e] = Elem<DT>::to_float(Elem<DT>::from_float(acc[i][j][4 * q + e]));
+            u[e] = Elem<DT>::to_float(Elem<DT>::from_float(acc[i][j][4 * q + 4 + e]));
+            y[e] = (g[e] / (1.f + __expf(-g[e]))) * u[e];
+          }
+          const uint2 packed = make_uint2(Elem<DT>::pack2(y[0], y[1]), Elem<DT>::pack2(y[2], y[3]));
+          *reinterpret_cast<uint2*>(a.out + static_cast<int64_t>(m) * a.ldo + oc) = packed;
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < B_BLK; ++j) {
     const int m = m0 + wm * kWaveM + 32 * j + col;
@@ -365,6 +411,25 @@ void launch_dt(int config, const LinearArgs& a, int blocks, hipStream_t s) {
   }
 }
 
+// The fused gate_up + SiLU launches (never split: K whole in every workgroup), for the
+// tile shapes `choose` can pick.
+template <int DT>
+bool launch_silu(int config, const LinearArgs& a, int blocks, hipStream_t s) {
+  switch (config) {
+    case 0:
+      linear_kernel<DT, 128, 192, 4, 2, 4, false, true><<<dim3(blocks), dim3(512), 0, s>>>(a);
+      return true;
+    case 6:
+      linear_kernel<DT, 128, 128, 4, 2, 3, false, true><<<dim3(blocks), dim3(512), 0, s>>>(a);
+      return true;
+    case 7:
+      linear_kernel<DT, 64, 128, 2, 4, 5, false, true><<<dim3(blocks), dim3(512), 0, s>>>(a);
+      return true;
+    default:
+      return false;
+  }
+}
+
 struct Choice {
   int config, splits;
 };
@@ -509,4 +574,46 @@ extern "C" const char* mi355x_linear_add_rms_norm(const void* x, int64_t ldx, co
       launch_reduce_add_rms<1, false>(partial, 1, o, ldo, r, ldr, g, m, n, fe, s);
   }
   return launch_status("reduce_add_rms");
+}
+
+extern "C" const char* mi355x_linear_silu_mul(const void* x, int64_t ldx, const void* w,
+                                              int64_t ldw, void* out, int64_t ldo, int64_t M,
+                                              int64_t width, int64_t K, int32_t cus,
+                                              int32_t config, int64_t dtype, void* stream) {
+  if (!x || !w || !out) return set_error("mi355x_linear_silu_mul: null pointer");
+  const int64_t N = 2 * width;
+  if (M <= 0 || width <= 0 || M > 4096 || width % 4 || K <= 0 || K % kBK || ldx < K ||
+      ldw < K || ldo < width || ldx % 8 || ldw % 8 || ldo % 4 || N > (int64_t(1) << 30) ||
+      (dtype != 0 && dtype != 1))
+    return set_error("mi355x_linear_silu_mul: unsupported shape (K % 64, width % 4, 16-byte rows)");
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(out, 8))
+    return set_error("mi355x_linear_silu_mul: misaligned operand");
+  // Tile shape measured on MI355X at the Qwen3-8B gate_up shape (width 12288, K 4096):
+  // 128 x 192 tiles from 129 rows up (62.6 us at 256 rows against 66.5 for hipBLASLt plus
+  // the SiLU pass), 128 x 128 for 65..128 rows, 64 x 128 below.
+  if (config < 0) config = M > 128 ? 0 : (M > 64 ? 6 : 7);
+  if (config >= kNumConfigs) return set_error("mi355x_linear_silu_mul: invalid tile configuration");
+  const TileConfig& t = kConfigs[config];
+  LinearArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.w = static_cast<const uint16_t*>(w);
+  a.out = static_cast<uint16_t*>(out);
+  a.ldx = ldx;
+  a.ldw = ldw;
+  a.ldo = ldo;
+  a.M = static_cast<int32_t>(M);
+  a.N = static_cast<int32_t>(N);
+  a.K = static_cast<int32_t>(K);
+  a.splits = 1;
+  a.k_per_split = static_cast<int32_t>(K);
+  a.tiles_m = static_cast<int32_t>(ceil_div(M, t.bm));
+  a.tiles_n = static_cast<int32_t>(ceil_div(N, t.bn));
+  a.groups = static_cast<int32_t>(ceil_div(a.tiles_n, 8) * 8);
+  const int64_t blocks = int64_t(a.groups) * a.tiles_m;
+  if (blocks > (int64_t(1) << 31) - 1) return set_error("mi355x_linear_silu_mul: grid too large");
+  auto s = static_cast<hipStream_t>(stream);
+  const bool ok = dtype == 0 ? launch_silu<0>(config, a, static_cast<int>(blocks), s)
+                             : launch_silu<1>(config, a, static_cast<int>(blocks), s);
+  if (!ok) return set_error("mi355x_linear_silu_mul: no fused kernel for this tiling");
+  return launch_status("linear_kernel (silu)");
 }

@@ -191,10 +191,10 @@ class Qwen3Model:
             # norm after the last layer): each a projection fused with its residual RMSNorm.
             x, residual = ops.linear_add_rms_norm(attn, layer.o_proj, residual,
                                                   layer.post_attention_layernorm, eps)
-            gate_up = ops.linear(x, layer.gate_up_proj)
+            # gate_up with SiLU x mul (one launch for decode batches)
+            act = ops.linear_silu_mul(x, layer.gate_up_proj)
             next_norm = self.layers[i + 1].input_layernorm if i + 1 < n_layers else self.norm
-            x, residual = ops.linear_add_rms_norm(ops.silu_and_mul(gate_up), layer.down_proj,
-                                                  residual, next_norm, eps)
+            x, residual = ops.linear_add_rms_norm(act, layer.down_proj, residual, next_norm, eps)
         hidden = x
         if logits_indices is not None:
             hidden = hidden.index_select(0, logits_indices)

@@ -294,6 +294,47 @@ def linear_add_rms_norm(x: torch.Tensor, weight: torch.Tensor, residual: torch.T
     return add_rms_norm(linear(x, weight), residual, norm_weight, eps)
 
 
+def uses_silu_kernel(rows: int, width: int, k: int) -> bool:
+    """Whether ``linear_silu_mul`` runs the fused gate_up + SiLU kernel for
+    ``[rows, k] x [2 width, k]^T``."""
+    return rows <= DECODE_MAX_ROWS and width % 4 == 0 and k % 64 == 0
+
+
+def decode_linear_silu_mul(x: torch.Tensor, weight: torch.Tensor,
+                           out: torch.Tensor | None = None, config: int = -1) -> torch.Tensor:
+    """``silu_and_mul(x @ weight.T)`` in one gfx950 launch: weight ``[2 W, K]`` (gate rows,
+    then up rows), result ``[M, W]``, bit-identical to ``decode_linear`` (unsplit) followed
+    by ``silu_and_mul``."""
+    _require_device(x, "decode_linear_silu_mul")
+    dt = dtype_code(x)
+    if (x.dim() != 2 or weight.dim() != 2 or x.stride(1) != 1 or not weight.is_contiguous()
+            or weight.dtype != x.dtype or weight.device != x.device
+            or weight.size(1) != x.size(1) or weight.size(0) % 2 != 0):
+        raise NativeError("invalid gate_up operands: expected x [M, K] and weight [2W, K]")
+    m, k = x.shape
+    width = weight.size(0) // 2
+    if out is None:
+        out = torch.empty((m, width), dtype=x.dtype, device=x.device)
+    elif (out.shape != (m, width) or out.dtype != x.dtype or out.stride(1) != 1
+          or out.device != x.device):
+        raise NativeError("invalid gate_up output")
+    check(lib().mi355x_linear_silu_mul(x.data_ptr(), x.stride(0), weight.data_ptr(),
+                                       weight.stride(0), out.data_ptr(), out.stride(0), m,
+                                       width, k, _native.device_cus(x.device), config, dt,
+                                       stream_of(x)), "decode_linear_silu_mul")
+    return out
+
+
+def linear_silu_mul(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """The MLP's ``silu_and_mul(linear(x, gate_up))`` (``mlp.rs``, ``ops.rs:53-61``):
+    decode-sized products in one fused launch, the rest as the two steps."""
+    if (x.is_cuda and x.dim() == 2 and x.stride(1) == 1 and weight.is_contiguous()
+            and weight.size(0) % 2 == 0
+            and uses_silu_kernel(x.size(0), weight.size(0) // 2, x.size(1))):
+        return decode_linear_silu_mul(x, weight)
+    return silu_and_mul(linear(x, weight))
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """``x @ weight.T``: decode-sized products on the gfx950 kernel, the rest on
     hipBLASLt (``src/layers/linear.rs:5-7``)."""
@@ -303,7 +344,8 @@ def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     return torch.nn.functional.linear(x, weight)
 
 
-__all__ = ["rms_norm", "add_rms_norm", "qk_norm", "silu_and_mul", "HalfSplitRope", "rope",
-           "qk_norm_rope_store", "decode_linear", "linear", "linear_add_rms_norm",
+__all__ = ["rms_norm", "add_rms_norm", "qk_norm", "silu_and_mul", "linear_silu_mul",
+           "HalfSplitRope", "rope", "qk_norm_rope_store", "decode_linear", "linear",
+           "linear_add_rms_norm", "decode_linear_silu_mul",
            "uses_decode_kernel", "NativeError",
            "_native"]

@@ -159,3 +159,35 @@ def test_fused_residual_norm_falls_back_outside_decode_sizes(gpu):
     got, _ = ops.linear_add_rms_norm(x, w, res_a, gamma, 1e-6)
     want, _ = ops.add_rms_norm(F.linear(x, w), res_b, gamma, 1e-6)
     assert torch.equal(got, want) and torch.equal(res_a, res_b)
+
+
+@pytest.mark.parametrize("config", [0, 6, 7])
+@pytest.mark.parametrize("m,width,k", [(256, 12288, 4096), (1, 12288, 4096), (97, 1000, 512),
+                                       (64, 196, 128)])
+def test_fused_gate_up_silu_equals_two_steps(gpu, config, m, width, k):
+    """mi355x_linear_silu_mul == decode_linear (same tiling, K unsplit) then silu_and_mul,
+    bit for bit, including widths that end inside a tile and ragged rows; and within the
+    tolerance of silu(g) * u on the float64 product."""
+    x, w = operands(m, 2 * width, k, torch.bfloat16, gpu, m + width + k + config)
+    fused = ops.decode_linear_silu_mul(x, w, config=config)
+    two_step = ops.silu_and_mul(ops.decode_linear(x, w, config=config, splits=1))
+    assert torch.equal(fused, two_step)
+    y = x.double() @ w.double().T
+    g, u = y[:, :width], y[:, width:]
+    want = g * torch.sigmoid(g) * u
+    a, b = fused.double().flatten(), want.flatten()
+    assert float(a @ b / (a.norm() * b.norm() + 1e-30)) > 0.9999
+    assert float((fused.double() - want).abs().max()) <= 2e-2 * float(want.abs().max()) + 1e-3
+
+
+def test_fused_gate_up_silu_routing_and_fallback(gpu):
+    """Decode-sized products take the fused launch; prefill-sized ones run hipBLASLt then
+    the SiLU pass, identical to the two calls."""
+    assert ops.uses_silu_kernel(256, 12288, 4096)
+    assert not ops.uses_silu_kernel(257, 12288, 4096)
+    x, w = operands(300, 512, 256, torch.bfloat16, gpu, 21)
+    assert torch.equal(ops.linear_silu_mul(x, w), ops.silu_and_mul(F.linear(x, w)))
+    x, w = operands(40, 512, 256, torch.bfloat16, gpu, 22)
+    assert torch.equal(ops.linear_silu_mul(x, w), ops.decode_linear_silu_mul(x, w))
+    with pytest.raises(NativeError, match="unsupported shape"):
+        ops.decode_linear_silu_mul(*operands(8, 2 * 66, 128, torch.bfloat16, gpu, 23))
