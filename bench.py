@@ -216,8 +216,23 @@ def _event_time_ms(fn, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
-def prefill_sections(dev, reps: int) -> dict:
-    """cfg3 ragged causal prefill and cfg4 paged prefill over a cached prefix (bf16 MFMA)."""
+def _cpu_median_ms(fn, runs: int = 3) -> tuple[float, int]:
+    """Median wall time of ``fn`` on the host cores (one warm-up run), and the threads used."""
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return sorted(times)[len(times) // 2], threads
+
+
+def prefill_sections(dev, reps: int, cpu: bool = True) -> dict:
+    """cfg3 ragged causal prefill and cfg4 paged prefill over a cached prefix (bf16 MFMA),
+    each with the oracle's torch-CPU fp32 restatement timed on a sample (reported baseline)."""
+    from oracle import attention as oatt
     from llm_infer_rust_amd.backend import (AttentionMetadata, AttentionSpec, BatchPhase,
                                             PrefillMetadata)
     from llm_infer_rust_amd.prefill import prepare_prefill_plan, run_prefill
@@ -247,6 +262,15 @@ def prefill_sections(dev, reps: int) -> dict:
                                   "TFLOP/s": round(tf, 2),
                                   "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
                                   "tokens": n}
+    if cpu:
+        sb = bounds[:3]  # the first two sequences
+        qs, ks, vs = (t[: sb[-1]].float().cpu() for t in (q, k, v))
+        cms, threads = _cpu_median_ms(lambda: oatt.prefill_ragged_torch(qs, ks, vs, sb))
+        sflops = 4 * 16 * 128 * sum(int(x) * (int(x) + 1) // 2 for x in lens[:2])
+        out["prefill_ragged_cfg3"]["cpu_baseline"] = {
+            "value": round(sflops / (cms * 1e-3) / 1e9, 2), "unit": "GFLOP/s", "cores": threads,
+            "kind": "port", "sample": f"first 2 of 8 sequences ({sb[-1]} tokens), torch-CPU fp32 "
+                                      "SDPA prefill restatement, median of 3"}
     del plan
     # cfg4: 16 requests, prefix ~ U[1024, 8192], extend ~ U[64, 512], Hq32/Hkv8, page 16.
     g = torch.Generator().manual_seed(4)
@@ -283,6 +307,29 @@ def prefill_sections(dev, reps: int) -> dict:
                                  "TFLOP/s": round(tf, 2),
                                  "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
                                  "extend_tokens": n, "prefix_tokens": int(pref.sum())}
+    if cpu:
+        # Two requests: their pages gathered into a compact CPU cache (page ids renumbered).
+        rows = [0, 1]
+        used = torch.cat([table[r, : int(pages_per[r])].long() for r in rows])
+        kcs = kc[used.to(dev)].float().cpu()
+        vcs = vc[used.to(dev)].float().cpu()
+        ctable = torch.zeros(len(rows), int(pages_per[rows].max()), dtype=torch.int64)
+        off = 0
+        for i, r in enumerate(rows):
+            m = int(pages_per[r])
+            ctable[i, :m] = torch.arange(off, off + m)
+            off += m
+        sb = [0] + torch.cumsum(ext[rows], 0).tolist()
+        qs = q[: sb[-1]].float().cpu()
+        cms, threads = _cpu_median_ms(lambda: oatt.prefill_with_cache_torch(
+            qs, kcs, vcs, ctable, sb, pref[rows].tolist(), page))
+        sflops = 4 * 32 * 128 * sum(int(ext[r]) * int(pref[r]) +
+                                    int(ext[r]) * (int(ext[r]) + 1) // 2 for r in rows)
+        out["prefill_paged_cfg4"]["cpu_baseline"] = {
+            "value": round(sflops / (cms * 1e-3) / 1e9, 2), "unit": "GFLOP/s", "cores": threads,
+            "kind": "port", "sample": f"2 of 16 requests ({sb[-1]} extend tokens over "
+                                      f"{int(pref[rows].sum())} cached), torch-CPU fp32 "
+                                      "restatement, median of 3"}
     return out
 
 
@@ -351,9 +398,11 @@ def ceilings_section(dev, w, reps: int) -> dict:
     return out
 
 
-def norm_sections(dev, reps: int) -> dict:
-    """cfg3 norms on 8192 x 1024 hidden rows and the 8192-token packed QKV (HBM-bound)."""
+def norm_sections(dev, reps: int, cpu: bool = True) -> dict:
+    """cfg3 norms on 8192 x 1024 hidden rows and the 8192-token packed QKV (HBM-bound), each
+    with the oracle's torch-CPU restatement timed on the full rows (reported baseline)."""
     from llm_infer_rust_amd import ops
+    from oracle import norms as onorms
 
     gd = torch.Generator(device=dev).manual_seed(33)
     # Rotate over buffer sets (> 1 GiB in total) so reads come from HBM, not from the
@@ -416,6 +465,19 @@ def norm_sections(dev, reps: int) -> dict:
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
                      "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if cpu:
+        xc, rc, wc = xs[0].cpu(), rs[0].cpu(), w.cpu()
+        pc = packs[0].cpu()
+        qc, kc = pc[:, :2048].reshape(-1, 16, 128), pc[:, 2048:3072].reshape(-1, 8, 128)
+        qwc, kwc = qw.cpu(), kw.cpu()
+        for name, fn in (("rms_norm", lambda: onorms.rms_norm_torch(xc, wc, 1e-6)),
+                         ("add_rms_norm", lambda: onorms.add_rms_norm_torch(xc, rc, wc, 1e-6)),
+                         ("qk_norm", lambda: onorms.qk_norm_torch(qc, kc, qwc, kwc, 1e-6))):
+            cms, threads = _cpu_median_ms(fn)
+            res[name]["cpu_baseline"] = {
+                "value": round(res[name]["bytes"] / (cms * 1e-3) / 1e9, 2), "unit": "GB/s",
+                "cores": threads, "kind": "port",
+                "sample": "full rows, torch-CPU restatement of ops.rs, median of 3"}
     return res
 
 
@@ -442,7 +504,8 @@ def main():
         return
     if args.only in ("prefill", "norms"):
         fn = prefill_sections if args.only == "prefill" else norm_sections
-        print(json.dumps({args.only: fn(dev, max(args.steps, 20))}))
+        print(json.dumps({args.only: fn(dev, max(args.steps, 20),
+                                         cpu=not args.no_cpu_baseline)}))
         return
     w = build_workload(args.seed, dev)
     if args.only == "ceilings":
@@ -532,9 +595,20 @@ def main():
     }
     if cpu is not None:
         result["cpu_baseline"] = cpu
+        # The K/V store on the host (base.rs:123-151: index_copy_ of the new rows into the
+        # cache), the same 64 rows into a 65,536-slot CPU pool.
+        kpool = torch.zeros(65536, HKV, D, dtype=torch.bfloat16)
+        vpool = torch.zeros_like(kpool)
+        kn, vn = w["knew"].cpu(), w["vnew"].cpu()
+        cloc = torch.randperm(65535, generator=torch.Generator().manual_seed(7))[:B] + 1
+        cms, threads = _cpu_median_ms(lambda: (kpool.index_copy_(0, cloc, kn),
+                                               vpool.index_copy_(0, cloc, vn)), runs=21)
+        result["kv_store"]["cpu_baseline"] = {
+            "value": round(sbytes / (cms * 1e-3) / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "sample": "64 rows into a 65,536-slot CPU pool, median of 21"}
     if not args.decode_only:
-        result["prefill"] = prefill_sections(dev, reps)
-        result["norms"] = norm_sections(dev, reps)
+        result["prefill"] = prefill_sections(dev, reps, cpu=not args.no_cpu_baseline)
+        result["norms"] = norm_sections(dev, reps, cpu=not args.no_cpu_baseline)
         ceil = ceilings_section(dev, w, min(reps, 50))
         ceil["decode_vs_gather"] = round(achieved / ceil["gather_2k_rows"]["GB/s"], 4)
         core = ceil["attention_core_random"]["TFLOP/s"]

@@ -11,9 +11,10 @@ Slots of a paged request follow the page table: token j of request r lives in
 slot table[r, j // P] * P + j % P (flashinfer_bridge.cpp:108-118 pages; the
 KV pool layout of src/engine/kvcache/pool.rs:81-104).
 
-The torch-CPU fp32 functions (``*_torch``) restate the same reference CPU
-path op for op in libtorch (index_select, repeat_interleave, bmm, masked_fill,
-softmax); they are the timed CPU baseline, not a checker.
+The torch-CPU fp32 functions (``*_torch``: decode, ragged prefill, prefill over a
+cached prefix) restate the same reference CPU path op for op in libtorch
+(index_select, repeat_interleave, bmm, masked_fill, softmax); they are the timed
+CPU baseline, not a checker.
 """
 from __future__ import annotations
 
@@ -148,4 +149,36 @@ def decode_with_cache_torch(q, k_cache, v_cache, block_table, lengths, page_size
         ck = flat_k.index_select(0, slots)
         cv = flat_v.index_select(0, slots)
         outs.append(attention_against_cache_torch(q[r:r + 1], ck, cv, length - 1, hq, hkv))
+    return torch.cat(outs, 0)
+
+
+def prefill_ragged_torch(q, k, v, cu_seqlens):
+    """Per-sequence causal attention, fp32 libtorch on CPU (the reference's SDPA prefill
+    plan, backend.rs:981-1142, without a cached prefix)."""
+    import torch
+
+    hq, hkv = q.size(1), k.size(1)
+    outs = []
+    for s, e in zip(list(cu_seqlens)[:-1], list(cu_seqlens)[1:]):
+        outs.append(attention_against_cache_torch(q[s:e], k[s:e], v[s:e], 0, hq, hkv))
+    return torch.cat(outs, 0)
+
+
+def prefill_with_cache_torch(q, k_cache, v_cache, block_table, cu_seqlens, prefixes,
+                             page_size: int):
+    """Extend queries over prefix + extend keys gathered from the paged cache, fp32 libtorch
+    on CPU (backend.rs:1297-1329)."""
+    import torch
+
+    hq, hkv, d = q.size(1), k_cache.size(2), q.size(2)
+    flat_k = k_cache.view(-1, hkv, d)
+    flat_v = v_cache.view(-1, hkv, d)
+    outs = []
+    for r, (s, e) in enumerate(zip(list(cu_seqlens)[:-1], list(cu_seqlens)[1:])):
+        length = int(prefixes[r]) + (e - s)
+        j = torch.arange(length)
+        slots = block_table[r].long()[j // page_size] * page_size + j % page_size
+        outs.append(attention_against_cache_torch(q[s:e], flat_k.index_select(0, slots),
+                                                  flat_v.index_select(0, slots),
+                                                  int(prefixes[r]), hq, hkv))
     return torch.cat(outs, 0)

@@ -6,7 +6,9 @@ src/layers/ops.rs:22-35  add_rms_norm: s = x_f32 + r_f32; normalise s (unrounded
 src/layers/ops.rs:39-51  qk_norm: rms_norm per head of q with q_w and of k with k_w
 Inputs are float32 arrays holding values already representable in the
 activation dtype; outputs are float32 before the final cast (use
-``oracle.bf16.round_to`` for the cast).
+``oracle.bf16.round_to`` for the cast). The ``*_torch`` functions restate the
+same op order in libtorch on CPU tensors of the activation dtype; they are the
+timed CPU baseline, not a checker.
 """
 from __future__ import annotations
 
@@ -28,3 +30,30 @@ def add_rms_norm_f32(x: np.ndarray, r: np.ndarray, w: np.ndarray, eps: float):
 
 def qk_norm_f32(q: np.ndarray, k: np.ndarray, qw: np.ndarray, kw: np.ndarray, eps: float):
     return rms_norm_f32(q, qw, eps), rms_norm_f32(k, kw, eps)
+
+
+def rms_norm_torch(x, w, eps: float):
+    """ops.rs:8-18 in libtorch: fp32 compute, cast back to x's dtype."""
+    import torch
+
+    xf = x.float()
+    var = xf.pow(2).mean(-1, keepdim=True)
+    return (xf * torch.rsqrt(var + eps) * w.float()).to(x.dtype)
+
+
+def add_rms_norm_torch(x, r, w, eps: float):
+    """ops.rs:22-35 in libtorch: returns (normalised, new residual)."""
+    s = x.float() + r.float()
+    return rms_norm_torch_f32(s, w, eps).to(x.dtype), s.to(x.dtype)
+
+
+def rms_norm_torch_f32(s, w, eps: float):
+    import torch
+
+    var = s.pow(2).mean(-1, keepdim=True)
+    return s * torch.rsqrt(var + eps) * w.float()
+
+
+def qk_norm_torch(q, k, qw, kw, eps: float):
+    """ops.rs:39-51 in libtorch: per-head RMSNorm of q and k."""
+    return rms_norm_torch(q, qw, eps), rms_norm_torch(k, kw, eps)

@@ -281,3 +281,40 @@ def test_torch_cpu_baseline_agrees_with_oracle():
     got = att.decode_with_cache_torch(torch.from_numpy(q), torch.from_numpy(kc),
                                       torch.from_numpy(vc), torch.from_numpy(table), lens, ps)
     np.testing.assert_allclose(got.numpy().reshape(b, hq, d), want, atol=1e-5)
+
+
+def test_torch_cpu_prefill_and_norm_baselines_agree_with_oracle():
+    """The timed torch-CPU restatements of prefill (ragged and over a cached prefix) and the
+    norms give the numpy oracle's results."""
+    rng = np.random.default_rng(6)
+    hq, hkv, d = 4, 2, 128
+    bounds = [0, 5, 17, 18]
+    n = bounds[-1]
+    q = rng.standard_normal((n, hq, d)).astype(np.float32)
+    k = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    want = att.prefill_ragged(q, k, v, bounds)
+    got = att.prefill_ragged_torch(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+                                   bounds)
+    np.testing.assert_allclose(got.numpy().reshape(want.shape), want, atol=1e-5)
+    ps, pages = 4, 30
+    kc = rng.standard_normal((pages, ps, hkv, d)).astype(np.float32)
+    vc = rng.standard_normal((pages, ps, hkv, d)).astype(np.float32)
+    table = rng.permutation(pages)[:24].reshape(3, 8).astype(np.int32)
+    prefixes = [3, 0, 9]
+    want = att.prefill_with_cache(q, kc, vc, table, bounds, prefixes, ps)
+    got = att.prefill_with_cache_torch(torch.from_numpy(q), torch.from_numpy(kc),
+                                       torch.from_numpy(vc), torch.from_numpy(table), bounds,
+                                       prefixes, ps)
+    np.testing.assert_allclose(got.numpy().reshape(want.shape), want, atol=1e-5)
+    x = rng.standard_normal((6, 256)).astype(np.float32)
+    r = rng.standard_normal((6, 256)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    np.testing.assert_allclose(norms.rms_norm_torch(torch.from_numpy(x), torch.from_numpy(w),
+                                                    1e-6).numpy(),
+                               norms.rms_norm_f32(x, w, 1e-6), rtol=1e-5, atol=1e-6)
+    out, res = norms.add_rms_norm_torch(torch.from_numpy(x), torch.from_numpy(r),
+                                        torch.from_numpy(w), 1e-6)
+    want_out, want_sum = norms.add_rms_norm_f32(x, r, w, 1e-6)
+    np.testing.assert_allclose(out.numpy(), want_out, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(res.numpy(), want_sum, rtol=1e-6, atol=1e-6)
