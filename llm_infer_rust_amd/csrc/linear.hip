@@ -1,9 +1,11 @@
 // Decode-step projection GEMMs on gfx950: out[M, N] = x[M, K] . w[N, K]^T.
 //
 // Replaces the reference's `x.matmul(w.T)` (src/layers/linear.rs:5-7, cuBLAS through
-// tch) for the decoder layer's QKV, o_proj, gate_up and down projections and the
-// lm_head when the batch is a decode batch (M <= 256 rows). Prefill-sized products
-// stay on hipBLASLt, which already runs them near the MFMA rate.
+// tch) for the decoder layer's QKV, o_proj and down projections when the batch is a
+// decode batch (M <= 256 rows), the last two optionally fused with the residual RMSNorm
+// that follows them, and the gate_up projection fused with SiLU x mul. Prefill-sized
+// products and the lm_head stay on hipBLASLt, which runs them near the MFMA rate or at a
+// weight-streaming rate this kernel does not beat.
 //
 // Why a kernel of its own: at M = 256 the four per-layer products carry 99 GFLOP
 // over 386 MB of weights, so they sit at the ridge between the MFMA rate and HBM
@@ -13,7 +15,7 @@
 // Design:
 //   * one workgroup computes a BM x BN output tile over a K range (split-K when
 //     the tiles alone cannot fill the chip; fp32 partials, then a reduce kernel);
-//   * the x and w tiles of each 64-wide K step stream through a 3-deep LDS ring filled
+//   * the x and w tiles of each 64-wide K step stream through a 3- to 5-deep LDS ring filled
 //     by direct global -> LDS copies (global_load_lds_dwordx4), rows of 128 bytes
 //     with the 16-byte chunks XOR-swizzled so the MFMA operand reads are
 //     conflict-free;
