@@ -11,8 +11,10 @@ Follows the reference layer sequence (``src/models/qwen3/model.rs:155-534``):
                 hidden = (silu(x W_gate^T) * x W_up^T) W_down^T
     logits = add_rms_norm(hidden, residual)[logits_indices] W_lm^T
 
-GEMMs are plain library GEMMs (torch -> hipBLASLt); everything around them is this library's
-HIP code. Configuration fields and defaults follow ``src/models/qwen3/config.rs:9-42``.
+For decode batches (at most 256 rows) the QKV, o_proj and down projections run on this
+library's projection kernel (o_proj and down fused with the residual RMSNorm that follows
+them) and gate_up runs fused with SiLU x mul; prefill-sized products and the lm_head are
+library GEMMs (torch -> hipBLASLt). Everything around them is this library's HIP code. Configuration fields and defaults follow ``src/models/qwen3/config.rs:9-42``.
 """
 from __future__ import annotations
 

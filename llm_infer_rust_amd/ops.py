@@ -216,8 +216,9 @@ def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 # columns go to the gfx950 projection kernel; long-K products (K > 4096) only from
 # DECODE_LONG_K_MIN_ROWS rows up. Everything else stays on hipBLASLt through
 # F.linear. The bounds come from timing both on MI355X at the Qwen3-8B shapes: the
-# kernel wins on QKV, o_proj and down (1.2-2.8x at 64-256 rows); hipBLASLt keeps
-# gate_up, the lm_head and prefill-sized products.
+# kernel wins on QKV, o_proj and down (1.2-2.8x at 64-256 rows); hipBLASLt keeps the
+# lm_head and prefill-sized products, and gate_up goes to the fused gate_up + SiLU entry
+# (``linear_silu_mul``).
 DECODE_MAX_ROWS = 256
 DECODE_MAX_N = 8192
 DECODE_LONG_K_MIN_ROWS = 32
