@@ -5,7 +5,8 @@
 * the full 256-request decode batch at the Qwen3-8B serving shape (page 16, GQA group 4,
   KV lengths 1024-1536, the largest captured decode-graph bucket);
 * paged prefill over a 65,536-token cached prefix next to a 1-token prefix and a 1-token
-  extend (query rows sampled: first, last and random).
+  extend (query rows sampled: first, last and random);
+* two decode plans and a prefill plan on three concurrent streams, equal to serial runs.
 Tolerance as in the per-kernel tests: max-abs <= 2e-2 and cosine similarity > 0.9999.
 """
 import numpy as np
@@ -121,3 +122,54 @@ def test_paged_prefill_64k_prefix_sampled_rows(gpu):
                                                 flat_k[slots], flat_v[slots], horizon - 1, hq,
                                                 hkv)
             assert_close(out[bounds[r] + i], want[0], f"req={r} row={i}")
+
+
+def test_plans_on_concurrent_streams_match_serial_runs(gpu):
+    """Two decode plans and a prefill plan launched on three streams at once (each plan owns
+    its workspace; the library keeps no shared device state) give the bytes of serial runs."""
+    rng = np.random.default_rng(77)
+    g = torch.Generator().manual_seed(77)
+    cases = []
+    for hq, page, lens in ((32, 16, rng.integers(200, 3000, size=48)),
+                           (16, 1, rng.integers(1, 2000, size=33))):
+        table, kc, vc = paged_pool(rng, g, gpu, lens, page, 8)
+        q = torch.randn(len(lens), hq, 128, generator=g).to(torch.bfloat16).to(gpu)
+        cache = BaseAttention()
+        cache.bind_kv_cache(kc, vc)
+        meta = AttentionMetadata(BatchPhase.DECODE,
+                                 block_table=torch.from_numpy(table).to(gpu),
+                                 cache_seqlens=torch.from_numpy(lens.astype(np.int32)).to(gpu))
+        batch = backend(gpu, hq, 8, page).prepare(meta, len(lens))
+        cases.append((batch, q, cache))
+    bounds = [0, 700, 1500]
+    n = bounds[-1]
+    pq = torch.randn(n, 16, 128, generator=g).to(torch.bfloat16).to(gpu)
+    pk = torch.randn(n, 8, 128, generator=g).to(torch.bfloat16).to(gpu)
+    pv = torch.randn(n, 8, 128, generator=g).to(torch.bfloat16).to(gpu)
+    pmeta = AttentionMetadata(BatchPhase.PREFILL,
+                              cu_seqlens_q=torch.tensor(bounds, dtype=torch.int32, device=gpu),
+                              prefix_lens=torch.zeros(2, dtype=torch.int32, device=gpu),
+                              block_table=torch.zeros(2, 128, dtype=torch.int32, device=gpu))
+    pbatch = backend(gpu, 16, 8, 16).prepare(pmeta, n)
+    pcache = BaseAttention()
+    serial = [b.forward(q, q, q, c).clone() for b, q, c in cases]
+    serial.append(pbatch.forward(pq, pk, pv, pcache).clone())
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(3)]
+    outs = []
+    for _ in range(3):  # a few rounds so launches overlap
+        for s in streams:
+            s.wait_stream(torch.cuda.current_stream())
+        round_outs = []
+        for s, (b, q, c) in zip(streams, cases):
+            with torch.cuda.stream(s):
+                round_outs.append(b.forward(q, q, q, c))
+        with torch.cuda.stream(streams[2]):
+            round_outs.append(pbatch.forward(pq, pk, pv, pcache))
+        for s in streams:
+            torch.cuda.current_stream().wait_stream(s)
+        outs.append(round_outs)
+    torch.cuda.synchronize()
+    for round_outs in outs:
+        for got, want in zip(round_outs, serial):
+            assert torch.equal(got, want)
