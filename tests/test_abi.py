@@ -167,3 +167,11 @@ def test_entry_points_reject_bad_arguments_before_launching(native):
     assert "null pointer" in err(lib.mi355x_sample(None, 2, 100, 100, 0, None, None, None, 1, 0,
                                                    None, None))
     assert "bad shape" in err(lib.mi355x_silu_mul(a, b, -1, 64, 0, None))
+
+
+def test_integration_guide_binds_every_declared_entry():
+    """The Rust FFI block a maintainer copies into the reference declares exactly the
+    entries of the C header."""
+    text = (ROOT / "INTEGRATION.md").read_text()
+    bound = set(re.findall(r"pub fn (mi355x_[a-z0-9_]+)\(", text))
+    assert bound == set(declared_functions())
