@@ -232,7 +232,6 @@ def _cpu_median_ms(fn, runs: int = 3) -> tuple[float, int]:
 def prefill_sections(dev, reps: int, cpu: bool = True) -> dict:
     """cfg3 ragged causal prefill and cfg4 paged prefill over a cached prefix (bf16 MFMA),
     each with the oracle's torch-CPU fp32 restatement timed on a sample (reported baseline)."""
-    from oracle import attention as oatt
     from llm_infer_rust_amd.backend import (AttentionMetadata, AttentionSpec, BatchPhase,
                                             PrefillMetadata)
     from llm_infer_rust_amd.prefill import prepare_prefill_plan, run_prefill
@@ -263,6 +262,8 @@ def prefill_sections(dev, reps: int, cpu: bool = True) -> dict:
                                   "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
                                   "tokens": n}
     if cpu:
+        from oracle import attention as oatt  # the CPU baseline only
+
         sb = bounds[:3]  # the first two sequences
         qs, ks, vs = (t[: sb[-1]].float().cpu() for t in (q, k, v))
         cms, threads = _cpu_median_ms(lambda: oatt.prefill_ragged_torch(qs, ks, vs, sb))
@@ -308,6 +309,8 @@ def prefill_sections(dev, reps: int, cpu: bool = True) -> dict:
                                  "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4),
                                  "extend_tokens": n, "prefix_tokens": int(pref.sum())}
     if cpu:
+        from oracle import attention as oatt  # the CPU baseline only
+
         # Two requests: their pages gathered into a compact CPU cache (page ids renumbered).
         rows = [0, 1]
         used = torch.cat([table[r, : int(pages_per[r])].long() for r in rows])
@@ -402,7 +405,6 @@ def norm_sections(dev, reps: int, cpu: bool = True) -> dict:
     """cfg3 norms on 8192 x 1024 hidden rows and the 8192-token packed QKV (HBM-bound), each
     with the oracle's torch-CPU restatement timed on the full rows (reported baseline)."""
     from llm_infer_rust_amd import ops
-    from oracle import norms as onorms
 
     gd = torch.Generator(device=dev).manual_seed(33)
     # Rotate over buffer sets (> 1 GiB in total) so reads come from HBM, not from the
@@ -466,6 +468,8 @@ def norm_sections(dev, reps: int, cpu: bool = True) -> dict:
         res[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
                      "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     if cpu:
+        from oracle import norms as onorms  # the CPU baseline only
+
         xc, rc, wc = xs[0].cpu(), rs[0].cpu(), w.cpu()
         pc = packs[0].cpu()
         qc, kc = pc[:, :2048].reshape(-1, 16, 128), pc[:, 2048:3072].reshape(-1, 8, 128)
