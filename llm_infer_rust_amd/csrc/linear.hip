@@ -439,28 +439,23 @@ struct Choice {
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Tile shape and split count: for each tile shape in order of preference, the fewest
-// K splits that give at least 3/4 of a workgroup per CU (none when the tiles already
-// cover 55% of the CUs); the first shape that needs at
-// most 4 splits and leaves each workgroup at most 4096 of K wins, else the one needing
-// the fewest splits. Measured on MI355X at the Qwen3-8B decode shapes (M = 64..256):
-// 64 x 128 tiles win on QKV and o_proj (QKV at 256 rows unsplit: 22.3 us against 26.9
-// for 128 x 128 tiles split twice plus the reduce), 128 x 128 tiles with 4 splits on the
-// long-K down projection (42.3 us; 64 x 128 tiles would need K ranges of 6144).
+// K splits that give at least 3/4 of a workgroup per CU; the first shape that needs at
+// most 4 splits wins, else the one needing the fewest. Measured on MI355X at the
+// Qwen3-8B decode shapes (M = 1..256) with the weights streamed from HBM (rotating over
+// more than 1 GB): 128 x 128 tiles with up to 4 splits beat smaller tiles with fewer
+// splits at 128-192 rows (QKV at 192 rows 27.7 us against 29.8 for 64 x 128 tiles
+// unsplit) and tie with them at 256 rows; the long-K down projection gains most.
 Choice choose(int64_t M, int64_t N, int64_t K, int cus) {
-  const int order[] = {7, 6, 0};
+  const int order[] = {6, 0, 7};
   const int64_t want = (3 * int64_t(cus)) / 4;
   Choice best{-1, 1 << 30};
   for (int c : order) {
     const TileConfig& t = kConfigs[c];
     const int64_t tiles = ceil_div(M, t.bm) * ceil_div(N, t.bn);
     int s = 1;
-    // Tiles covering 55% of the CUs stay unsplit: the partials and the reduce cost more
-    // than the idle CUs (QKV at 192 rows: 144 tiles unsplit 22.1 us, split twice 29.9;
-    // o_proj at 256 rows: 128 tiles split twice 19.1 us, unsplit 22.4).
-    if (tiles * 100 < int64_t(cus) * 55)
-      while (s < 8 && tiles * s < want && K % (int64_t(2 * s) * kBK) == 0) s *= 2;
+    while (s < 8 && tiles * s < want && K % (int64_t(2 * s) * kBK) == 0) s *= 2;
     if (K % (int64_t(s) * kBK)) continue;
-    if (s <= 4 && K / s <= 4096) return {c, s};
+    if (s <= 4) return {c, s};
     if (s < best.splits) best = {c, s};
   }
   return best.config >= 0 ? best : Choice{7, 1};
