@@ -39,6 +39,7 @@ constexpr int kTileK = 64;                    // keys per tile
 constexpr int kQPerWave = 32;                 // queries per wave
 constexpr int kWaves = 8;                     // waves per workgroup
 constexpr int kStages = 4;                    // LDS ring depth (tiles)
+constexpr int kAhead = kStages - 1;           // tiles in flight ahead of the one computed
 constexpr int kTileBytes = kTileK * kD * 2;   // 16 KB per K or V tile
 constexpr int kStageBytes = 2 * kTileBytes;   // K + V
 constexpr float kLog2e = 1.4426950408889634f;
@@ -91,19 +92,15 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return Elem<DT>::pack2(a, b);
 }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
-// c + a.lo * b.lo + a.hi * b.hi with fp32 accumulation (v_dot2_f32_bf16 / _f16).
+// Eight 16-bit values times c, rounded back to the element type (round to nearest even).
 template <int DT>
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  if constexpr (DT == 0) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                           __builtin_bit_cast(bf16x2_t, b), c, false);
-  } else {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b),
-                                  c, false);
-  }
+__device__ __forceinline__ uint4 scale_row8(const uint4& x, float c) {
+  auto sc = [&](uint32_t w) {
+    return Elem<DT>::pack2(Elem<DT>::to_float(static_cast<uint16_t>(w & 0xffff)) * c,
+                           Elem<DT>::to_float(static_cast<uint16_t>(w >> 16)) * c);
+  };
+  return make_uint4(sc(x.x), sc(x.y), sc(x.z), sc(x.w));
 }
 
 // ---------------------------------------------------------------------------
@@ -188,6 +185,10 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
 #pragma unroll
     for (int s = 0; s < 8; ++s) qreg[s] = ld128(qp + 16 * s + 8 * half);
     wait_vmem_loads();
+    // Fold the softmax scale (and log2 e) into the query once per item, so the tile
+    // loop's scores come out of the matrix cores already in the exp2 domain.
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qreg[s] = scale_row8<DT>(qreg[s], a.scale_log2);
   }
 
   const uint32_t lds_base = lds_address(lds);
@@ -256,6 +257,20 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
     lane_v[j] = v_req + static_cast<int64_t>(row_in_group) * a.v_sn + vc * 8;
   }
   const int pages_per_tile = PAGED && fast_pages ? kTileK / a.page_size : 0;
+  const int last_page = PAGED ? (kv_len - 1) / a.page_size : 0;
+  // Paged fast path: the page id of each of this wave's row groups, for the tile
+  // issued next. They are loaded one loop iteration before their copies are issued,
+  // so the scalar loads' latency is hidden behind a tile of compute instead of
+  // stalling the copy issue right after the barrier.
+  int ids[kGroupsPerWave];
+  auto load_ids = [&](int t) {
+#pragma unroll
+    for (int j = 0; j < kGroupsPerWave; ++j) {
+      const int g = wave * kGroupsPerWave + j;
+      const int p = min(t * pages_per_tile + (4 * g) / a.page_size, last_page);
+      ids[j] = *((const __attribute__((address_space(4))) int32_t*)(a.indices) + rq.page_base + p);
+    }
+  };
   auto issue_fast = [&](int t, int stage) {
     const uint32_t sbase = lds_base + stage * kStageBytes;
 #pragma unroll
@@ -263,10 +278,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
       const int g = wave * kGroupsPerWave + j;
       int64_t first;  // key (ragged) or slot (paged) of the group's first row
       if constexpr (PAGED) {
-        const int p = t * pages_per_tile + (4 * g) / a.page_size;
-        const int page =
-            *((const __attribute__((address_space(4))) int32_t*)(a.indices) + rq.page_base + p);
-        first = static_cast<int64_t>(page) * a.page_size + (4 * g) % a.page_size;
+        first = static_cast<int64_t>(ids[j]) * a.page_size + (4 * g) % a.page_size;
       } else {
         first = t * kTileK + 4 * g;
       }
@@ -274,11 +286,16 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
       copy_to_lds(lane_v[j] + first * a.v_sn, sbase + kTileBytes + g * 1024);
     }
   };
+  // Issues tile t; in paged mode the ids must hold tile t's page ids, and on return
+  // they hold tile t + 1's.
   auto issue = [&](int t, int stage) {
     if (fast_pages && t + 1 < n_tiles)
       issue_fast(t, stage);
     else
       issue_general(t, stage);
+    if constexpr (PAGED) {
+      if (fast_pages) load_ids(t + 1);
+    }
   };
 
   // Read side offsets (bytes within a stage).
@@ -300,12 +317,19 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
-  float m = -1e30f, l = 0.f;
+  // m: this lane's reference max (log2 domain); every S^T accumulator starts at -m,
+  // so the scores leave the matrix cores as s - m and p = 2^(s - m) needs no VALU fma.
+  float m = 0.f, l = 0.f;
+  floatx16 negm;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) negm[r] = 0.f;
   const int my_q = wq0 + col;
   const int my_horizon = rq.prefix + my_q;
 
   // One 64-key tile per step: S^T = K Q^T (two 32-key blocks), mask and row max, lazy
   // rescale, P^T = 2^(s scale - m), O^T += V^T P^T.
+  // One 64-key tile per step: S^T = K Q^T - m (two 32-key blocks), mask and row max,
+  // lazy rescale, P^T = 2^(S^T), O^T += V^T P^T.
   auto compute = [&](int t, int stage) {
     const int k0 = t * kTileK;
     if (!(wave_active && k0 <= wave_last_key)) return;
@@ -319,13 +343,9 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
             sb + (32 * T + col) * 256 + (((2 * kk + half) ^ (col & 15)) * 16));
     floatx16 s[2];
 #pragma unroll
-    for (int T = 0; T < 2; ++T)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[T][r] = 0.f;
-#pragma unroll
     for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
-      for (int T = 0; T < 2; ++T) s[T] = Mfma<DT>::run(kf[T][kk], qreg[kk], s[T]);
+      for (int T = 0; T < 2; ++T) s[T] = Mfma<DT>::run(kf[T][kk], qreg[kk], kk == 0 ? negm : s[T]);
     uint4 vf[4][4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
@@ -356,55 +376,60 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
     {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
                                                         false, false);
-      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * a.scale_log2;
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max of s - m
     }
-    // Lazy rescale: the reference max m only moves when some row's max exceeds it by
-    // more than 8, so p = 2^(s - m) <= 2^8 and O / l are rescaled rarely.
-    if (__any(mx > m + 8.f)) {
-      const float m_new = fmaxf(m, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-      m = m_new;
+    // Lazy rescale: m moves on the first tile (to the row max) and afterwards only when
+    // some row's max exceeds it by more than 8, so p = 2^(s - m) <= 2^8 and O / l are
+    // rescaled rarely. Every tile starts at key 0, which each query sees, so mx is finite.
+    if (t == 0 || __any(mx > 8.f)) {
+      const float shift = t == 0 ? mx : fmaxf(mx, 0.f);
+      const float alpha = __builtin_amdgcn_exp2f(-shift);
+      m += shift;
       l *= alpha;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[0][r] -= shift;
+        s[1][r] -= shift;
+        negm[r] = -m;
+      }
     }
     uint4 pb[4];
-    const uint32_t ones = pack2<DT>(1.f, 1.f);
+    float ls[4] = {0.f, 0.f, 0.f, 0.f};  // independent partial row sums (fp32 p)
 #pragma unroll
     for (int T = 0; T < 2; ++T)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         float p[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          p[i] = __builtin_amdgcn_exp2f(fmaf(s[T][8 * hh + i], a.scale_log2, -m));
-        uint4& w4 = pb[2 * T + hh];
-        w4 = make_uint4(pack2<DT>(p[0], p[1]), pack2<DT>(p[2], p[3]), pack2<DT>(p[4], p[5]),
-                        pack2<DT>(p[6], p[7]));
-        l = dot2<DT>(w4.x, ones, l);
-        l = dot2<DT>(w4.y, ones, l);
-        l = dot2<DT>(w4.z, ones, l);
-        l = dot2<DT>(w4.w, ones, l);
+        for (int i = 0; i < 8; ++i) {
+          p[i] = __builtin_amdgcn_exp2f(s[T][8 * hh + i]);
+          ls[i & 3] += p[i];
+        }
+        pb[2 * T + hh] = make_uint4(pack2<DT>(p[0], p[1]), pack2<DT>(p[2], p[3]),
+                                    pack2<DT>(p[4], p[5]), pack2<DT>(p[6], p[7]));
       }
+    l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
       for (int db = 0; db < 4; ++db) o[db] = Mfma<DT>::run(vf[kk][db], pb[kk], o[db]);
   };
 
+  if constexpr (PAGED) {
+    if (fast_pages) load_ids(0);
+  }
 #pragma unroll
-  for (int st = 0; st < STAGES - 1; ++st)
+  for (int st = 0; st < kAhead; ++st)
     if (st < n_tiles) issue(st, st);
-  int read_stage = 0, fill_stage = STAGES - 1;  // ring positions of tile t and t + STAGES - 1
   for (int t = 0; t < n_tiles; ++t) {
-    wait_tiles_ahead<kCopiesPerTile, STAGES - 2>(min(STAGES - 2, n_tiles - 1 - t));
+    wait_tiles_ahead<kCopiesPerTile, kAhead - 1>(min(kAhead - 1, n_tiles - 1 - t));
     __syncthreads();
-    if (t + STAGES - 1 < n_tiles) issue(t + STAGES - 1, fill_stage);
-    compute(t, read_stage);
-    read_stage = read_stage == STAGES - 1 ? 0 : read_stage + 1;
-    fill_stage = fill_stage == STAGES - 1 ? 0 : fill_stage + 1;
+    if (t + kAhead < n_tiles) issue(t + kAhead, (t + kAhead) % STAGES);
+    compute(t, t % STAGES);
   }
 
   if (!wave_active || my_q >= rq.q_len) return;
