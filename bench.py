@@ -28,6 +28,18 @@ import torch
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 COPY_CAL_BYTES = 256 << 20
+# Prefill / norm sections time a fixed number of launches (after a fixed warm-up), so
+# their figures do not depend on --steps; sustained prefill runs clock down under the
+# MFMA load, and these counts measure that sustained rate.
+PREFILL_WARMUP = 100
+SECTION_REPS = 100
+# The device's power management settles over tens of milliseconds of load (measured:
+# cfg4 prefill launches fall from ~550 to ~410 us over the first ~100 launches, decode
+# from ~113 to ~109 us), so every timed region is preceded by a fixed device warm-up of
+# the same work, and the decode launches of the roofline figure are timed over their own
+# fixed count. The headline value still times exactly --steps steps after --warmup.
+DEVICE_WARMUP_STEPS = 300
+ROOFLINE_REPS = 200
 LAYERS = 4  # KV pools the decode steps rotate over (4 x 16 GiB)
 TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "decode_cfg2_traffic.txt")
@@ -216,6 +228,75 @@ def _event_time_ms(fn, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
+def _graph_time_us(fn, launches: int = 100, replays: int = 20) -> float:
+    """Per-launch device time of ``fn`` with the host out of the loop: ``launches`` calls
+    are captured in one hipGraph and the graph is replayed ``replays`` times between HIP
+    events, so the figure is kernel time plus the graph's inter-node gaps, not the rate
+    at which Python issues launches."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm-up on the capture stream (allocator, lazy init)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(launches):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) * 1e3 / (replays * launches)
+
+
+def replan_section(dev) -> dict:
+    """Steady-state decode re-planning (the per-step host work of a served decode batch):
+    an existing plan re-made from host lengths (no device read-back), median host time per
+    call, at cfg2 (64 rows, page 1) and at the 256-row Qwen3-8B bucket (page 16,
+    ~1,000-1,600-token contexts). The first, cold call is reported separately."""
+    from llm_infer_rust_amd.backend import (AttentionMetadata, AttentionSpec, BatchPhase,
+                                            DecodeHostMetadata, prepare_decode_plan)
+
+    out = {}
+    for name, rows, page, lo, hi, hq in (("cfg2_64x_page1", 64, 1, 512, 4096, 16),
+                                         ("cfg5_256x_page16", 256, 16, 1024, 1536, 32)):
+        g = torch.Generator().manual_seed(rows)
+        lens = torch.randint(lo, hi + 1, (rows,), generator=g, dtype=torch.int32)
+        cols = (hi + page - 1) // page
+        table = torch.randint(1, 1 << 20, (rows, cols), generator=g, dtype=torch.int32)
+        spec = AttentionSpec(hq, 8, 128, torch.bfloat16, dev)
+        table_d, lens_d = table.to(dev), lens.to(dev)
+        host = lens.tolist()
+
+        def meta():
+            return AttentionMetadata(BatchPhase.DECODE, block_table=table_d, cache_seqlens=lens_d,
+                                     decode_host=DecodeHostMetadata(host))
+
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        plan = prepare_decode_plan(None, meta(), spec, page, graph=False)
+        torch.cuda.synchronize()
+        cold = (time.perf_counter() - t0) * 1e3
+        times = []
+        for i in range(60):
+            m = meta()
+            t0 = time.perf_counter()
+            prepare_decode_plan(plan, m, spec, page, graph=False)
+            times.append((time.perf_counter() - t0) * 1e3)
+        torch.cuda.synchronize()
+        out[name] = {"warm_ms": round(statistics.median(times[10:]), 4),
+                     "cold_ms": round(cold, 3), "rows": rows, "page_size": page}
+        del plan
+    return out
+
+
 def _cpu_median_ms(fn, runs: int = 3) -> tuple[float, int]:
     """Median wall time of ``fn`` on the host cores (one warm-up run), and the threads used."""
     threads = min(os.cpu_count() or 1, 16)
@@ -254,6 +335,8 @@ def prefill_sections(dev, reps: int, cpu: bool = True) -> dict:
     spec = AttentionSpec(16, 8, 128, torch.bfloat16, dev)
     plan = prepare_prefill_plan(None, meta, PrefillMetadata(bounds, [0] * 8), spec, 16)
     o = torch.empty_like(q)
+    for _ in range(PREFILL_WARMUP):
+        run_prefill(plan, q, k, v, o)
     ms = _event_time_ms(lambda: run_prefill(plan, q, k, v, o), reps)
     flops = 4 * 16 * 128 * sum(int(x) * (int(x) + 1) // 2 for x in lens)
     tf = flops / (ms * 1e-3) / 1e12
@@ -300,6 +383,8 @@ def prefill_sections(dev, reps: int, cpu: bool = True) -> dict:
     spec = AttentionSpec(32, 8, 128, torch.bfloat16, dev)
     plan = prepare_prefill_plan(None, meta, PrefillMetadata(bounds, pref.tolist()), spec, page)
     o = torch.empty_like(q)
+    for _ in range(PREFILL_WARMUP):
+        run_prefill(plan, q, kc, vc, o)
     ms = _event_time_ms(lambda: run_prefill(plan, q, kc, vc, o), reps)
     flops = 4 * 32 * 128 * sum(int(e) * int(p) + int(e) * (int(e) + 1) // 2
                                for e, p in zip(ext, pref))
@@ -457,6 +542,12 @@ def norm_sections(dev, reps: int, cpu: bool = True) -> dict:
         outs[i % sets].copy_(xs[i % sets])
 
     res = {}
+    gx, gr = dx[0], dr[0]
+    g_us = _graph_time_us(lambda: ops.add_rms_norm(gx, gr, w4, 1e-6))
+    res["add_rms_norm_256x4096_graph"] = {
+        "us": round(g_us, 3), "bytes": 4 * 256 * 4096 * 2,
+        "GB/s": round(4 * 256 * 4096 * 2 / (g_us * 1e-6) / 1e9, 1),
+        "note": "one buffer set replayed from a hipGraph (L2/MALL-resident after the first)"}
     for name, fn, nbytes in (
             ("rms_norm", rms, 2 * 8192 * 1024 * 2),
             ("add_rms_norm", add_rms, 4 * 8192 * 1024 * 2),
@@ -508,8 +599,7 @@ def main():
         return
     if args.only in ("prefill", "norms"):
         fn = prefill_sections if args.only == "prefill" else norm_sections
-        print(json.dumps({args.only: fn(dev, max(args.steps, 20),
-                                         cpu=not args.no_cpu_baseline)}))
+        print(json.dumps({args.only: fn(dev, SECTION_REPS, cpu=not args.no_cpu_baseline)}))
         return
     w = build_workload(args.seed, dev)
     if args.only == "ceilings":
@@ -539,7 +629,7 @@ def main():
         c.write_kv(w["knew"], w["vnew"], w["loc"])
         run_decode(plan, w["q"], c.k_cache, c.v_cache, out)
 
-    for i in range(args.warmup):
+    for i in range(DEVICE_WARMUP_STEPS + args.warmup):
         step(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -549,7 +639,9 @@ def main():
     step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
 
     # Decode kernels alone, HIP events on the current (launch) stream.
-    reps = max(args.steps, 20)
+    reps = ROOFLINE_REPS
+    for i in range(reps // 2):
+        run_decode(plan, w["q"], w["kcs"][i % LAYERS], w["vcs"][i % LAYERS], out)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -610,9 +702,16 @@ def main():
         result["kv_store"]["cpu_baseline"] = {
             "value": round(sbytes / (cms * 1e-3) / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port", "sample": "64 rows into a 65,536-slot CPU pool, median of 21"}
+    # Small kernels by graph replay (device time per launch, no Python launch overhead).
+    kv_graph_us = _graph_time_us(lambda: caches[0].write_kv(w["knew"], w["vnew"], w["loc"]))
+    for c in caches:
+        c.check_write_errors()
+    result["kv_store"]["graph_us"] = round(kv_graph_us, 3)
+    result["kv_store"]["graph_GB/s"] = round(sbytes / (kv_graph_us * 1e-6) / 1e9, 2)
+    result["replan"] = replan_section(dev)
     if not args.decode_only:
-        result["prefill"] = prefill_sections(dev, reps, cpu=not args.no_cpu_baseline)
-        result["norms"] = norm_sections(dev, reps, cpu=not args.no_cpu_baseline)
+        result["prefill"] = prefill_sections(dev, SECTION_REPS, cpu=not args.no_cpu_baseline)
+        result["norms"] = norm_sections(dev, SECTION_REPS, cpu=not args.no_cpu_baseline)
         ceil = ceilings_section(dev, w, min(reps, 50))
         ceil["decode_vs_gather"] = round(achieved / ceil["gather_2k_rows"]["GB/s"], 4)
         core = ceil["attention_core_random"]["TFLOP/s"]

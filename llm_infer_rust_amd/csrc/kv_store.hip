@@ -109,7 +109,10 @@ extern "C" const char* mi355x_store_kv(const void* k, const void* v, void* kc, v
     return set_error("mi355x_store_kv: invalid geometry");
   if (tokens == 0) return nullptr;
   if (!k || !v || !kc || !vc || !loc) return set_error("mi355x_store_kv: null pointer");
-  if (tokens * heads * width >= (int64_t(1) << 40))
+  // One thread per element (or per 16-byte chunk); the grid is a single uint32 x
+  // dimension of 256-thread blocks, so keep every launch below 2^32 threads.
+  if (tokens > (int64_t(1) << 40) / heads || tokens * heads > (int64_t(1) << 40) / width ||
+      tokens * heads * width >= (int64_t(1) << 32) - 256)
     return set_error("mi355x_store_kv: launch too large");
   const bool vec = width % 8 == 0 && kt % 8 == 0 && kh % 8 == 0 && vt % 8 == 0 && vh % 8 == 0 &&
                    aligned(k, 16) && aligned(v, 16) && aligned(kc, 16) && aligned(vc, 16);

@@ -226,7 +226,7 @@ DECODE_LONG_K_MIN_ROWS = 32
 
 def uses_decode_kernel(rows: int, n: int, k: int) -> bool:
     """Whether ``linear`` routes an ``[rows, k] x [n, k]^T`` product to the gfx950 kernel."""
-    return (rows <= DECODE_MAX_ROWS and n <= DECODE_MAX_N and n % 4 == 0 and k % 64 == 0
+    return (0 < rows <= DECODE_MAX_ROWS and n <= DECODE_MAX_N and n % 4 == 0 and k % 64 == 0
             and (k <= 4096 or rows >= DECODE_LONG_K_MIN_ROWS))
 
 
@@ -275,8 +275,9 @@ def linear_add_rms_norm(x: torch.Tensor, weight: torch.Tensor, residual: torch.T
     n = weight.size(0)
     if (x.is_cuda and x.dim() == 2 and x.stride(1) == 1 and weight.is_contiguous()
             and uses_decode_kernel(m, n, k) and n % 8 == 0 and 128 < n // 8 <= 1024
-            and residual.dim() == 2 and residual.shape == (m, n) and residual.stride(1) == 1
-            and residual.dtype == x.dtype and residual.stride(0) % 8 == 0):
+            and x.stride(0) % 8 == 0 and residual.dim() == 2 and residual.shape == (m, n)
+            and residual.stride(1) == 1 and residual.dtype == x.dtype
+            and residual.device == x.device and residual.stride(0) % 8 == 0):
         _require_device(x, "linear_add_rms_norm")
         dt = dtype_code(x)
         _check_weight(x, norm_weight, n)
@@ -298,7 +299,7 @@ def linear_add_rms_norm(x: torch.Tensor, weight: torch.Tensor, residual: torch.T
 def uses_silu_kernel(rows: int, width: int, k: int) -> bool:
     """Whether ``linear_silu_mul`` runs the fused gate_up + SiLU kernel for
     ``[rows, k] x [2 width, k]^T``."""
-    return rows <= DECODE_MAX_ROWS and width % 4 == 0 and k % 64 == 0
+    return 0 < rows <= DECODE_MAX_ROWS and width % 4 == 0 and k % 64 == 0
 
 
 def decode_linear_silu_mul(x: torch.Tensor, weight: torch.Tensor,

@@ -130,15 +130,21 @@ def test_graph_replays_match_eager(gpu):
 
 
 
-@pytest.mark.parametrize("m,n,k", [(256, 4096, 4096), (256, 4096, 12288), (100, 2048, 1024),
-                                   (1, 4096, 4096), (64, 2048, 64)])
-def test_fused_residual_norm_equals_separate_passes(gpu, m, n, k):
+@pytest.mark.parametrize("m,n,k,dtype", [(256, 4096, 4096, torch.bfloat16),
+                                         (256, 4096, 12288, torch.bfloat16),
+                                         (100, 2048, 1024, torch.bfloat16),
+                                         (1, 4096, 4096, torch.bfloat16),
+                                         (64, 2048, 64, torch.bfloat16),
+                                         (256, 4096, 4096, torch.float16),
+                                         (64, 2048, 64, torch.float16)])
+def test_fused_residual_norm_equals_separate_passes(gpu, m, n, k, dtype):
     """mi355x_linear_add_rms_norm == decode_linear then add_rms_norm, bit for bit, for split
-    (fp32 partials reduced in the norm pass) and unsplit (K = 64) projections."""
-    x, w = operands(m, n, k, torch.bfloat16, gpu, m * 7 + n + k)
+    (fp32 partials reduced in the norm pass) and unsplit (K = 64) projections, in bf16 and
+    fp16."""
+    x, w = operands(m, n, k, dtype, gpu, m * 7 + n + k)
     g = torch.Generator().manual_seed(n + k)
-    residual = torch.randn(m, n, generator=g).to(torch.bfloat16).to(gpu)
-    gamma = (torch.rand(n, generator=g) + 0.5).to(torch.bfloat16).to(gpu)
+    residual = torch.randn(m, n, generator=g).to(dtype).to(gpu)
+    gamma = (torch.rand(n, generator=g) + 0.5).to(dtype).to(gpu)
     res_sep = residual.clone()
     y = ops.decode_linear(x, w)
     want, _ = ops.add_rms_norm(y, res_sep, gamma, 1e-6)
@@ -161,14 +167,15 @@ def test_fused_residual_norm_falls_back_outside_decode_sizes(gpu):
     assert torch.equal(got, want) and torch.equal(res_a, res_b)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("config", [0, 6, 7])
 @pytest.mark.parametrize("m,width,k", [(256, 12288, 4096), (1, 12288, 4096), (97, 1000, 512),
                                        (64, 196, 128)])
-def test_fused_gate_up_silu_equals_two_steps(gpu, config, m, width, k):
+def test_fused_gate_up_silu_equals_two_steps(gpu, config, m, width, k, dtype):
     """mi355x_linear_silu_mul == decode_linear (same tiling, K unsplit) then silu_and_mul,
-    bit for bit, including widths that end inside a tile and ragged rows; and within the
-    tolerance of silu(g) * u on the float64 product."""
-    x, w = operands(m, 2 * width, k, torch.bfloat16, gpu, m + width + k + config)
+    bit for bit, including widths that end inside a tile and ragged rows, in bf16 and fp16;
+    and within the tolerance of silu(g) * u on the float64 product."""
+    x, w = operands(m, 2 * width, k, dtype, gpu, m + width + k + config)
     fused = ops.decode_linear_silu_mul(x, w, config=config)
     two_step = ops.silu_and_mul(ops.decode_linear(x, w, config=config, splits=1))
     assert torch.equal(fused, two_step)
@@ -191,3 +198,8 @@ def test_fused_gate_up_silu_routing_and_fallback(gpu):
     assert torch.equal(ops.linear_silu_mul(x, w), ops.decode_linear_silu_mul(x, w))
     with pytest.raises(NativeError, match="unsupported shape"):
         ops.decode_linear_silu_mul(*operands(8, 2 * 66, 128, torch.bfloat16, gpu, 23))
+    # An empty batch routes to the two-step path like F.linear.
+    x0, w0 = operands(1, 512, 256, torch.bfloat16, gpu, 24)
+    assert not ops.uses_silu_kernel(0, 256, 256) and not ops.uses_decode_kernel(0, 512, 256)
+    assert ops.linear_silu_mul(x0[:0], w0).shape == (0, 256)
+    assert ops.linear(x0[:0], w0).shape == (0, 512)

@@ -1,14 +1,16 @@
 """Qwen3 model and serving engine on the GPU against the fp32 Qwen3 oracle.
 
-Greedy checks are teacher-forced: each token the GPU engine emits must be an argmax of the
-oracle's logits for the same prefix within a stated tolerance (bf16 activations cannot
-reproduce fp32 near-ties, so an exact token list would test rounding, not plumbing). Logits
-must also agree in direction (cos-sim) with the oracle's.
+Greedy checks: the GPU engine's free-running token list must equal the oracle's (fp32 on the
+same bf16 weights) up to the first step whose oracle top-1/top-2 gap lies inside the measured
+bf16 logit error (a genuine near tie, where bf16 arithmetic may pick either); and, teacher-
+forced over every step, each emitted token is an argmax of the oracle's logits for the same
+prefix within that error. Logits must also agree in direction (cos-sim) with the oracle's.
 """
 import numpy as np
 import pytest
 import torch
 
+from engine_helpers import RecordingEngine
 from llm_infer_rust_amd.engine import Engine, EngineConfig
 from llm_infer_rust_amd.model import Qwen3Config, Qwen3Model
 from llm_infer_rust_amd.sampling import SamplingParams
@@ -65,23 +67,37 @@ def test_engine_greedy_matches_oracle(gpu, use_graphs):
 
 
 def test_decode_graph_logits_match_eager(gpu):
+    """Every decode step's logits from a graph replay (3 live rows in a 4-row bucket, one pad
+    row at page 0 / slot 0) against the eager forward of the same rows: greedy sampling keeps
+    both runs on the same tokens, so each step compares the same inputs. A pad row writing a
+    live slot, or a position off by one, changes the logits of later steps far beyond the
+    bf16 tolerance used here."""
     model, _ = build(TINY, 3, gpu)
-    outs = []
+    runs = []
     for graphs in (True, False):
-        eng = Engine(model, EngineConfig(max_running_req=4, max_seq_len=128,
-                                         use_graphs=graphs, seed=9))
+        eng = RecordingEngine(model, EngineConfig(max_running_req=4, max_seq_len=128,
+                                                  use_graphs=graphs, seed=9,
+                                                  graph_batch_sizes=(4,)))
         rng = np.random.default_rng(4)
         for n in (7, 33, 20):
-            eng.add_request(rng.integers(0, TINY.vocab_size, n),
-                            SamplingParams(temperature=0.7, top_k=50, top_p=0.9, max_tokens=6))
+            eng.add_request(rng.integers(0, TINY.vocab_size, n), SamplingParams(max_tokens=8))
         eng.run_until_complete()
-        outs.append([r.output for r in sorted(eng.finished, key=lambda r: r.uid)])
+        if graphs:
+            assert eng.stats["graph_steps"] == eng.stats["decode_steps"] > 0
+        else:
+            assert eng.stats["graph_steps"] == 0
+        runs.append(eng.records)
         del eng
         torch.cuda.synchronize()
-    # Both paths run the same kernels on the same plans' data, with the same sampler seed.
-    assert all(len(o) == 6 for o in outs[0])
-    agree = sum(a == b for x, y in zip(*outs) for a, b in zip(x, y))
-    assert agree >= 0.8 * 18, outs
+    graph, eager = runs
+    assert len(graph) == len(eager)
+    for step, ((ug, lg, pg), (ue, le, pe)) in enumerate(zip(graph, eager)):
+        assert ug == ue and pg == pe, step  # same rows, same greedy tokens
+        a, b = lg.double(), le.double()
+        cos = torch.nn.functional.cosine_similarity(a, b, dim=1)
+        err = float((a - b).abs().max())
+        assert float(cos.min()) > 0.99999, (step, cos)
+        assert err <= 1e-2 * float(b.abs().max()) + 4e-3, (step, err)
 
 
 def test_prefill_logits_match_oracle(gpu):
@@ -112,14 +128,50 @@ def test_prefill_logits_match_oracle(gpu):
     assert picked
 
 
-def test_config1_shape_bf16_greedy_tracks_oracle(gpu):
-    # Qwen3-0.6B dimensions: 128 random prompt ids, 64 greedy tokens through the engine (graphs).
+def test_config1_shape_greedy_tokens_match_oracle(gpu):
+    """Config 1 (Qwen3-0.6B dimensions, 128 random prompt ids, 64 greedy tokens) through the
+    engine with graph decode, against the fp32 oracle's own free-running greedy run on the
+    same bf16 weights."""
     cfg = Qwen3Config.qwen3_0_6b()
     model, oracle = build(cfg, 0, gpu, std=0.02)
-    eng = Engine(model, EngineConfig(max_running_req=1, max_seq_len=256,
-                                     graph_batch_sizes=(1,)))
+    eng = RecordingEngine(model, EngineConfig(max_running_req=1, max_seq_len=256,
+                                              graph_batch_sizes=(1,)))
     prompt = np.random.default_rng(0).integers(0, cfg.vocab_size, 128)
     req = eng.add_request(prompt, SamplingParams(max_tokens=64))
     eng.run_until_complete()
     assert len(req.output) == 64
-    check_teacher_forced(oracle, prompt, req.output, tol=0.08)
+    # Teacher-forced over all 64 steps: the oracle's logits for the GPU's own prefix. At a
+    # step whose logits differ by at most e (max-abs), bf16 arithmetic can only pick a
+    # token whose oracle logit is within 2 e of the maximum.
+    oracle.reset()
+    want = [oracle.forward(prompt, 0)[-1]]
+    pos = prompt.size
+    for t in req.output[:-1]:
+        want.append(oracle.forward(np.array([t]), pos)[-1])
+        pos += 1
+    errs, exact = [], 0
+    for (_, got, picked), ref in zip(eng.records, want):
+        e = float(np.abs(got[0].double().numpy() - ref).max())
+        assert e < 0.05 * float(np.abs(ref).max()) + 0.02
+        deficit = float(ref.max() - ref[picked[0]])
+        assert deficit <= 2 * e, (deficit, e)
+        exact += int(deficit == 0.0)
+        errs.append(e)
+    # Free-running: the oracle's own greedy run from the same prompt. The token lists must
+    # agree up to the first step where the oracle's top-1/top-2 gap is inside 2 e (a genuine
+    # near tie; past it the two sequences legitimately differ).
+    oracle.reset()
+    logits, pos, ref, gaps = want[0], prompt.size, [], []
+    oracle.forward(prompt, 0)
+    for _ in range(64):
+        top2 = np.sort(logits)[-2:]
+        gaps.append(float(top2[1] - top2[0]))
+        ref.append(int(np.argmax(logits)))
+        logits = oracle.forward(np.array([ref[-1]]), pos)[-1]
+        pos += 1
+    same = next((i for i, (a, b) in enumerate(zip(req.output, ref)) if a != b), 64)
+    print(f"config 1: {same}/64 leading greedy tokens identical to the oracle's, {exact}/64 "
+          f"exact argmax teacher-forced; logit error max {max(errs):.4f}; smallest oracle "
+          f"gap {min(gaps):.4f}")
+    if same < 64:
+        assert gaps[same] <= 2 * errs[same], (same, gaps[same], errs[same])
