@@ -289,6 +289,20 @@ const char* mi355x_linear_silu_mul(const void* x, int64_t ldx, const void* w, in
 int64_t mi355x_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t cus,
                                       int32_t config, int32_t splits);
 
+/* mi355x_linear without a workspace argument and without any allocation: the
+ * split-K partials go to a 32 MiB device array held by the library on each GPU
+ * it runs on (until the process ends). No counterpart in the reference: it is
+ * for callers that cannot allocate (code under hipGraph capture without a
+ * memory pool, serving loops that forbid hipMalloc). Same arguments, tiling and
+ * results as mi355x_linear; fails with an error when the chosen tiling needs
+ * more than 32 MiB of partials (mi355x_linear_workspace_bytes tells). All calls
+ * on one GPU share that array, so calls that overlap on one GPU (different
+ * streams, or host threads) race; calls ordered on one stream are safe. */
+const char* mi355x_linear_noalloc(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                                  void* out, int64_t ldo, int64_t M, int64_t N, int64_t K,
+                                  int32_t cus, int32_t config, int32_t splits, int64_t dtype,
+                                  void* stream);
+
 /* ------------------------------------------------------------------------
  * Sampling.
  * ------------------------------------------------------------------------ */

@@ -86,6 +86,9 @@ SIGNATURES: dict[str, tuple] = {
                                               c_i64, c_i64, c_i64, c_void_p, c_i64, c_i32,
                                               c_i64, c_void_p]),
     "mi355x_linear_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64, c_i32, c_i32, c_i32]),
+    "mi355x_linear_noalloc": (c_char_p, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64,
+                                         c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i64,
+                                         c_void_p]),
     "mi355x_linear_silu_mul": (c_char_p, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64,
                                           c_i64, c_i64, c_i64, c_i32, c_i32, c_i64,
                                           c_void_p]),

@@ -26,6 +26,7 @@
 //   * workgroups that share a weight tile (different M tiles of it) are placed on the
 //     same XCD (workgroup i runs on XCD i mod 8), so the tile is fetched from HBM once.
 #include <algorithm>
+#include <mutex>
 #include <cstdint>
 
 #include "common.h"
@@ -541,6 +542,61 @@ extern "C" const char* mi355x_linear(const void* x, int64_t ldx, const void* w, 
                                      void* stream) {
   return run_linear(x, ldx, w, ldw, out, ldo, M, N, K, workspace, workspace_bytes, cus, config,
                     splits, dtype, false, nullptr, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of mi355x_linear: the split-K partials go to a file-scope
+// device array instead of a caller workspace. Each GPU the library runs on holds its
+// own copy of the array (kLinearScratchBytes) until the process ends. In host code the
+// array's name is only a stand-in for its symbol; the device address of each GPU's copy
+// is looked up once per device (hipGetSymbolAddress, with that device current) and that
+// pointer is what the kernels receive.
+// ---------------------------------------------------------------------------
+namespace mi355x {
+namespace {
+constexpr int64_t kLinearScratchBytes = int64_t(32) << 20;
+static __device__ __align__(256) uint8_t scratch[kLinearScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch array, looked up on first use.
+const char* scratch_for_current_device(void** out) {
+  int device = 0;
+  hipError_t st = hipGetDevice(&device);
+  if (st != hipSuccess) return hip_error(st, "hipGetDevice");
+  if (device < 0 || device >= kMaxDevices) return set_error("mi355x_linear_noalloc: device id");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    st = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (st != hipSuccess) return hip_error(st, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return nullptr;
+}
+}  // namespace
+}  // namespace mi355x
+
+extern "C" const char* mi355x_linear_noalloc(const void* x, int64_t ldx, const void* w,
+                                             int64_t ldw, void* out, int64_t ldo, int64_t M,
+                                             int64_t N, int64_t K, int32_t cus, int32_t config,
+                                             int32_t splits, int64_t dtype, void* stream) {
+  const int64_t need = mi355x_linear_workspace_bytes(M, N, K, cus, config, splits);
+  if (need < 0) return set_error("mi355x_linear: unsupported shape (K % 64, N % 4, 16-byte rows)");
+  if (need > kLinearScratchBytes)
+    return set_error("mi355x_linear_noalloc: split-K partials exceed the 32 MiB scratch "
+                     "(use mi355x_linear with a workspace)");
+  void* ws = nullptr;
+  if (need > 0) {
+    if (const char* e = scratch_for_current_device(&ws)) return e;
+  }
+  // Every split writes its whole [M, N] slice of partials before the reduce reads it,
+  // so the scratch needs no clearing between calls.
+  return run_linear(x, ldx, w, ldw, out, ldo, M, N, K, ws, need, cus, config, splits, dtype,
+                    false, nullptr, static_cast<hipStream_t>(stream));
 }
 
 extern "C" const char* mi355x_linear_add_rms_norm(const void* x, int64_t ldx, const void* w,
