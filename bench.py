@@ -470,6 +470,22 @@ def ceilings_section(dev, w, reps: int) -> dict:
     ms = timed(gather, reps)
     out["gather_2k_rows"] = {"us": round(ms * 1e3, 2), "bytes": nbytes,
                              "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    # In-flight sweep of the same gather (rows per wave x workgroups), at the decode's
+    # random slots and at the same slots sorted (row-buffer locality, same bytes).
+    lib.mi355x_calib_gather_depth.restype = ctypes.c_char_p
+    sorted_slots = torch.sort(slots).values
+    sweep = {}
+    for label, sl in (("random", slots), ("sorted", sorted_slots)):
+        for depth, blocks in ((1, 1024), (2, 1024), (4, 1024), (8, 1024), (8, 256), (2, 4096)):
+            def g(i, sl=sl, depth=depth, blocks=blocks):
+                check(lib.mi355x_calib_gather_depth(
+                    ctypes.c_void_p(w["kcs"][i % LAYERS].data_ptr()),
+                    ctypes.c_void_p(w["vcs"][i % LAYERS].data_ptr()),
+                    ctypes.c_void_p(sl.data_ptr()), rows, depth, blocks,
+                    ctypes.c_void_p(sink.data_ptr()), stream))
+            ms = timed(g, reps)
+            sweep[f"{label}_d{depth}_wg{blocks}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    out["gather_sweep_GB/s"] = sweep
     ms = timed(stream_read, reps)
     out["stream_read"] = {"us": round(ms * 1e3, 2), "bytes": nbytes,
                           "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}

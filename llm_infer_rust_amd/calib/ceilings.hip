@@ -53,17 +53,23 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+// The decode memory pattern without arithmetic: per row (token) the 2 KiB K row and the
+// 2 KiB V row at a page-table slot, read into registers. Each wave keeps DEPTH rows
+// (DEPTH * 4 KiB, 4 x 16-byte loads per lane per row) in flight per loop trip; the grid is
+// `blocks` workgroups of 8 waves. A structure unlike the decode kernel's (register loads,
+// many waves per CU, no LDS ring), so its rate bounds the pattern, not one kernel.
+template <int DEPTH>
 __global__ __launch_bounds__(512) void gather_rows(const uint4* __restrict__ k,
                                                    const uint4* __restrict__ v,
                                                    const int32_t* __restrict__ slots, int rows,
                                                    uint32_t* sink) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int stride = gridDim.x * 8 * 2;
+  const int stride = gridDim.x * 8 * DEPTH;
   uint32_t acc = 0;
-  for (int r0 = (blockIdx.x * 8 + wave) * 2; r0 < rows; r0 += stride) {
-    uint4 x[2][4];
+  for (int r0 = (blockIdx.x * 8 + wave) * DEPTH; r0 < rows; r0 += stride) {
+    uint4 x[DEPTH][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < DEPTH; ++i) {
       const int64_t s = slots[min(r0 + i, rows - 1)];
       x[i][0] = k[s * 128 + lane];
       x[i][1] = k[s * 128 + 64 + lane];
@@ -71,7 +77,7 @@ __global__ __launch_bounds__(512) void gather_rows(const uint4* __restrict__ k,
       x[i][3] = v[s * 128 + 64 + lane];
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) acc ^= x[i][0].x ^ x[i][1].y ^ x[i][2].z ^ x[i][3].w;
+    for (int i = 0; i < DEPTH; ++i) acc ^= x[i][0].x ^ x[i][1].y ^ x[i][2].z ^ x[i][3].w;
   }
   if (acc == 0x9e3779b9u) sink[0] = acc;
 }
@@ -218,9 +224,28 @@ __global__ __launch_bounds__(512, 1) void attention_core(float* sink, int iters)
 // Each entry point launches one measurement kernel on `stream`; NULL on success.
 extern "C" __attribute__((visibility("default"))) const char* mi355x_calib_gather(
     const void* k, const void* v, const int32_t* slots, int32_t rows, void* sink, void* stream) {
-  gather_rows<<<1024, 512, 0, static_cast<hipStream_t>(stream)>>>(
+  gather_rows<2><<<1024, 512, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint4*>(k), static_cast<const uint4*>(v), slots, rows,
       static_cast<uint32_t*>(sink));
+  return hipGetLastError() == hipSuccess ? nullptr : "gather launch failed";
+}
+
+// The same gather with DEPTH rows in flight per wave (1, 2, 4 or 8) over `blocks`
+// workgroups: the in-flight sweep that shows where the pattern saturates.
+extern "C" __attribute__((visibility("default"))) const char* mi355x_calib_gather_depth(
+    const void* k, const void* v, const int32_t* slots, int32_t rows, int32_t depth,
+    int32_t blocks, void* sink, void* stream) {
+  auto s = static_cast<hipStream_t>(stream);
+  auto kp = static_cast<const uint4*>(k);
+  auto vp = static_cast<const uint4*>(v);
+  auto out = static_cast<uint32_t*>(sink);
+  switch (depth) {
+    case 1: gather_rows<1><<<blocks, 512, 0, s>>>(kp, vp, slots, rows, out); break;
+    case 2: gather_rows<2><<<blocks, 512, 0, s>>>(kp, vp, slots, rows, out); break;
+    case 4: gather_rows<4><<<blocks, 512, 0, s>>>(kp, vp, slots, rows, out); break;
+    case 8: gather_rows<8><<<blocks, 512, 0, s>>>(kp, vp, slots, rows, out); break;
+    default: return "gather depth must be 1, 2, 4 or 8";
+  }
   return hipGetLastError() == hipSuccess ? nullptr : "gather launch failed";
 }
 
