@@ -169,9 +169,59 @@ def test_entry_points_reject_bad_arguments_before_launching(native):
     assert "bad shape" in err(lib.mi355x_silu_mul(a, b, -1, 64, 0, None))
 
 
-def test_integration_guide_binds_every_declared_entry():
-    """The Rust FFI block a maintainer copies into the reference declares exactly the
-    entries of the C header."""
-    text = (ROOT / "INTEGRATION.md").read_text()
-    bound = set(re.findall(r"pub fn (mi355x_[a-z0-9_]+)\(", text))
-    assert bound == set(declared_functions())
+# C parameter / return type (after removing names) -> the Rust FFI type that matches it.
+C_TO_RUST = {
+    "void*": "*mut c_void", "const void*": "*const c_void", "int64_t": "i64", "int32_t": "i32",
+    "int": "c_int", "bool": "bool", "double": "f64", "uint64_t": "u64", "void": "()",
+    "const char*": "*const c_char", "int32_t*": "*mut i32", "const int32_t*": "*const i32",
+    "int64_t*": "*mut i64", "const int64_t*": "*const i64", "const float*": "*const f32",
+}
+
+
+def header_signatures():
+    """name -> (return type, [parameter types]) of every declaration in the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for ret, name, params in re.findall(
+            r"([A-Za-z_][\w ]*?\**)\s*\b(mi355x_\w+)\s*\(([^)]*)\)\s*;", text):
+        types = []
+        for p in [p.strip() for p in params.split(",") if p.strip() and p.strip() != "void"]:
+            p = re.sub(r"\s+", " ", p)
+            m = re.match(r"(.*?)(\**)\s*\b\w+$", p)
+            types.append((m.group(1).strip() + m.group(2)).replace(" *", "*"))
+        out[name] = (re.sub(r"\s+", " ", ret.strip()).replace(" *", "*"), types)
+    return out
+
+
+def crate_signatures():
+    """name -> (return type, [parameter types]) of the mi355x_sys crate's extern block."""
+    text = (ROOT / "rust" / "mi355x_sys" / "src" / "lib.rs").read_text()
+    out = {}
+    for name, params, ret in re.findall(r"pub fn (mi355x_\w+)\(([^)]*)\)\s*(?:->\s*([^;]+))?;",
+                                        text):
+        types = [re.sub(r"\s+", " ", p.split(":", 1)[1].strip())
+                 for p in params.split(",") if p.strip()]
+        out[name] = ((ret or "()").strip(), types)
+    return out
+
+
+def test_rust_crate_declares_every_entry_with_matching_types():
+    """The FFI crate a maintainer adds to the reference (rust/mi355x_sys) declares exactly the
+    entries of the C header, each parameter and return type the Rust equivalent of the C one."""
+    header, crate = header_signatures(), crate_signatures()
+    assert set(header) == set(declared_functions())
+    assert set(crate) == set(header)
+    for name, (ret, params) in header.items():
+        cret, cparams = crate[name]
+        assert C_TO_RUST[ret] == cret, (name, ret, cret)
+        assert [C_TO_RUST[p] for p in params] == cparams, (name, params, cparams)
+
+
+def test_rust_backend_uses_only_declared_entries():
+    """The drop-in backend module calls only entries the crate declares."""
+    text = (ROOT / "rust" / "attention_mi355x.rs").read_text()
+    used = set(re.findall(r"sys::(mi355x_\w+)\(", text))
+    assert used and used <= set(crate_signatures())
+    for needed in ("mi355x_decode_prepare", "mi355x_decode_run", "mi355x_decode_plan_drop",
+                   "mi355x_prefill_prepare", "mi355x_prefill_run", "mi355x_prefill_plan_drop"):
+        assert needed in used
