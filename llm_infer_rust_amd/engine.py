@@ -8,11 +8,13 @@ Mirrors the parts of the reference engine that feed the attention hot path:
 * the serial scheduler step (``src/scheduler/scheduler.rs:205-271``): one prefill batch (FIFO,
   token budget, the last request chunked when it does not fit), then one decode step over every
   running request;
-* batch metadata (``src/engine/batch_context.rs:216-360``, ``src/scheduler/decode.rs:168-422``):
-  int32 ``block_table`` / ``cache_seqlens`` / ``cu_seqlens_q`` / ``prefix_lens``, slots
-  ``page * page_size + offset`` for ``write_loc``. The host keeps the block table, lengths and
-  positions incrementally (a request's row changes only when it gains a page) and uploads one
-  pinned staging block per step; the planner reads host lengths, never device ones;
+* batch metadata from ``batch.BatchContext`` / ``batch.DecodeTables``
+  (``src/engine/batch_context.rs:216-360``, ``src/scheduler/decode.rs:168-422``): int32
+  ``block_table`` (-1 past a request's pages) / ``cache_seqlens`` / ``cu_seqlens_q`` /
+  ``prefix_lens``, slots ``page * page_size + offset`` for ``write_loc``. Decode block-table
+  rows persist across steps and change only when a row gets another request or a page; one
+  pinned staging block is uploaded per step and the planner reads host lengths, never device
+  ones;
 * ``DecodeGraphRunner`` (``src/engine/graph.rs:26-329``): fixed input buffers per captured batch
   size, pad rows pointing at the reserved page 0 (length 1, slot 0 skipped by the K/V store),
   and the attention plan re-made outside the graph before each replay
@@ -28,6 +30,7 @@ import numpy as np
 import torch
 
 from .backend import AttentionMetadata, BatchPhase, DecodeHostMetadata
+from .batch import BatchContext, BatchRequest, DecodeBatch, DecodeRequest, DecodeTables
 from .kv_cache import KVCacheLayout, KVCachePool, ModelError
 from .model import Qwen3Model
 from .sampling import Sampler, SamplingParams
@@ -140,20 +143,20 @@ class Engine:
         cfg, mcfg = self.cfg, model.cfg
         self.device = model.device
         self.page_size = cfg.page_size
-        self.cols = -(-cfg.max_seq_len // cfg.page_size)
+        self.cols = -(-cfg.max_seq_len // cfg.page_size)  # block-table columns
         num_pages = cfg.num_pages or cfg.max_running_req * self.cols
         self.pool = KVCachePool(KVCacheLayout(mcfg.num_layers, num_pages, cfg.page_size,
                                               mcfg.num_kv_heads, mcfg.head_dim),
                                 model.dtype, self.device)
         model.bind_kv_cache(self.pool, reserved_slot=0)
         self.pages = PageAllocator(num_pages)
+        self.batches = BatchContext(cfg.max_running_req, cfg.max_seq_len, cfg.page_size)
+        self.tables = DecodeTables(cfg.max_running_req, cfg.max_seq_len, cfg.page_size)
         self.sampler = Sampler(cfg.seed)
         self.waiting: list[Request] = []
         self.running: list[Request] = []
         self.finished: list[Request] = []
         self._next_uid = 0
-        # Host mirror of the decode block table, one row per running request (by uid).
-        self._rows: dict[int, np.ndarray] = {}
         self._staging = torch.empty(0, dtype=torch.int64, pin_memory=True)
         self.graphs: dict[int, _DecodeGraph] = {}
         self.stats = {"prefill_batches": 0, "decode_steps": 0, "graph_steps": 0}
@@ -177,16 +180,7 @@ class Engine:
     def _ensure_pages(self, req: Request, tokens: int) -> None:
         need = -(-tokens // self.page_size) - len(req.pages)
         if need > 0:
-            new = self.pages.alloc(need)
-            start = len(req.pages)
-            req.pages.extend(new)
-            row = self._rows.setdefault(req.uid, np.zeros(self.cols, np.int32))
-            row[start:start + need] = new
-
-    def _slots(self, req: Request, start: int, stop: int) -> np.ndarray:
-        pos = np.arange(start, stop)
-        pages = np.asarray(req.pages, np.int64)
-        return pages[pos // self.page_size] * self.page_size + pos % self.page_size
+            req.pages.extend(self.pages.alloc(need))
 
     def _pack(self, arrays) -> int:
         """Copy int32/int64 arrays into the pinned staging buffer as 8-byte words."""
@@ -233,33 +227,26 @@ class Engine:
         return picked
 
     def _run_prefill(self, picked: list[tuple[Request, int]]) -> None:
-        ids, pos, loc, cu, prefixes, table = [], [], [], [0], [], []
-        last_rows = []
+        rows = []
         for req, take in picked:
             if not req.admitted:
                 req.admitted = True
                 self.waiting.remove(req)
                 self.running.append(req)
-            start = req.cursor
-            self._ensure_pages(req, start + take)
-            ids.append(req.prompt[start:start + take])
-            pos.append(np.arange(start, start + take))
-            loc.append(self._slots(req, start, start + take))
-            prefixes.append(start)
-            cu.append(cu[-1] + take)
-            table.append(self._rows[req.uid])
-            if start + take == req.prompt.size:
-                last_rows.append(cu[-1] - 1)
-        n = cu[-1]
+            self._ensure_pages(req, req.cursor + take)
+            rows.append(BatchRequest(req.prompt, req.cursor, req.cursor + take, req.pages))
+        b = self.batches.prepare_prefill(rows)
+        # Logits only for requests whose prompt ends in this batch (possibly none).
+        last = np.asarray([i for (req, take), i in zip(picked, b.logits_indices)
+                           if req.cursor + take == req.prompt.size], np.int64)
         ids_d, pos_d, loc_d, idx_d, cu_d, prefix_d, table_d = self._upload(
-            np.concatenate(ids), np.concatenate(pos), np.concatenate(loc),
-            np.asarray(last_rows, np.int64), np.asarray(cu, np.int32),
-            np.asarray(prefixes, np.int32), np.stack(table).astype(np.int32))
+            b.input_ids, b.positions, b.write_loc, last, b.cu_seqlens_q, b.prefix_lens,
+            b.block_table)
         meta = AttentionMetadata(BatchPhase.PREFILL, write_loc=loc_d, cu_seqlens_q=cu_d,
                                  prefix_lens=prefix_d, block_table=table_d,
-                                 host_cu_seqlens_q=cu, host_prefix_lens=prefixes)
-        batch = self.model.attention.prepare(meta, n)
-        # Logits only for requests whose prompt ends in this batch (possibly none).
+                                 host_cu_seqlens_q=b.cu_seqlens_q.tolist(),
+                                 host_prefix_lens=b.prefix_lens.tolist())
+        batch = self.model.attention.prepare(meta, int(b.cu_seqlens_q[-1]))
         logits = self.model.forward(ids_d, pos_d, batch, loc_d, idx_d)
         del batch
         for req, take in picked:
@@ -274,29 +261,28 @@ class Engine:
         return [r for r in self.running if r.cursor == r.prompt.size and r.output
                 and not r.finished()]
 
+    def _decode_batch(self, rows: list[Request]) -> DecodeBatch:
+        reqs = []
+        for req in rows:
+            length = req.cached_len + 1   # the fed token sits at position cached_len
+            self._ensure_pages(req, length)
+            reqs.append(DecodeRequest(req.uid, length, req.output[-1], req.pages))
+        return self.tables.prepare(reqs)
+
     def _run_decode(self, rows: list[Request]) -> None:
         n = len(rows)
-        pos = np.empty(n, np.int64)
-        ids = np.empty(n, np.int64)
-        for i, req in enumerate(rows):
-            p = req.cached_len          # position of the token being fed
-            self._ensure_pages(req, p + 1)
-            pos[i] = p
-            ids[i] = req.output[-1]
-        pages = np.asarray([req.pages[p // self.page_size] for req, p in zip(rows, pos)],
-                           np.int64)
-        loc = pages * self.page_size + pos % self.page_size
-        lens = (pos + 1).astype(np.int32)
+        b = self._decode_batch(rows)
         graph = self._graph_for(n)
         if graph is not None:
-            self._replay(graph, rows, ids, pos, loc, lens)
+            self._replay(graph, b)
             logits = graph.logits[:n]
             self.stats["graph_steps"] += 1
         else:
-            table = np.stack([self._rows[r.uid] for r in rows])
-            ids_d, pos_d, loc_d, lens_d, table_d = self._upload(ids, pos, loc, lens, table)
+            ids_d, pos_d, loc_d, lens_d, table_d = self._upload(
+                b.input_ids, b.positions, b.write_loc, b.cache_seqlens, b.block_table)
             meta = AttentionMetadata(BatchPhase.DECODE, decode_host=DecodeHostMetadata(
-                lens.tolist()), write_loc=loc_d, block_table=table_d, cache_seqlens=lens_d)
+                b.cache_seqlens.tolist()), write_loc=loc_d, block_table=table_d,
+                cache_seqlens=lens_d)
             batch = self.model.attention.prepare(meta, n)
             logits = self.model.forward(ids_d, pos_d, batch, loc_d)
             del batch
@@ -318,7 +304,6 @@ class Engine:
             self.finished.append(req)
             self.pages.release(req.pages)
             req.pages = []
-            self._rows.pop(req.uid, None)
 
     # ------------------------------------------------------------------ graphs
     def _bucket_sizes(self) -> list[int]:
@@ -362,21 +347,20 @@ class Engine:
             torch.cuda.synchronize(self.device)
             self.graphs[bs] = g
 
-    def _replay(self, g: _DecodeGraph, rows: list[Request], ids: np.ndarray, pos: np.ndarray,
-                loc: np.ndarray, lens: np.ndarray) -> None:
-        n, bs = len(rows), g.bs
+    def _replay(self, g: _DecodeGraph, b: DecodeBatch) -> None:
+        n, bs = b.input_ids.size, g.bs
         pad = bs - n
-        table = np.zeros((bs, self.cols), np.int32)  # pad rows: page 0
-        for i, req in enumerate(rows):
-            table[i] = self._rows[req.uid]
-        # Pad rows: token 0 at position 0, slot 0 (the reserved slot), length 1.
-        arrays = (np.concatenate([ids, np.zeros(pad, np.int64)]),
-                  np.concatenate([pos, np.zeros(pad, np.int64)]),
-                  np.concatenate([loc, np.zeros(pad, np.int64)]),
-                  np.concatenate([lens, np.ones(pad, np.int32)]), table)
+        # Pad rows (``graph.rs:285-320``): token 1 at position 0, the reserved slot 0, length 1,
+        # every block-table column page 0.
+        table = np.zeros((bs, self.cols), np.int32)
+        table[:n] = b.block_table
+        arrays = (np.concatenate([b.input_ids, np.ones(pad, np.int64)]),
+                  np.concatenate([b.positions, np.zeros(pad, np.int64)]),
+                  np.concatenate([b.write_loc, np.zeros(pad, np.int64)]),
+                  np.concatenate([b.cache_seqlens, np.ones(pad, np.int32)]), table)
         total = self._pack(arrays)
         g.block.copy_(self._staging[:total], non_blocking=True)  # one copy into the graph inputs
-        g.state.prepare_replay(DecodeHostMetadata(lens.tolist()))
+        g.state.prepare_replay(DecodeHostMetadata(b.cache_seqlens.tolist()))
         g.graph.replay()
 
     # ------------------------------------------------------------------ loop

@@ -11,6 +11,7 @@ import pytest
 import torch
 
 from engine_helpers import RecordingEngine
+from llm_infer_rust_amd.batch import BatchRequest
 from llm_infer_rust_amd.engine import Engine, EngineConfig
 from llm_infer_rust_amd.model import Qwen3Config, Qwen3Model
 from llm_infer_rust_amd.sampling import SamplingParams
@@ -112,10 +113,9 @@ def test_prefill_logits_match_oracle(gpu):
     eng.running.append(req)
     req.admitted = True
     eng._ensure_pages(req, 50)
-    loc = eng._slots(req, 0, 50)
+    b = eng.batches.prepare_prefill([BatchRequest(prompt, 0, 50, req.pages)])
     ids_d, pos_d, loc_d, cu_d, pre_d, tab_d = eng._upload(
-        prompt.astype(np.int64), np.arange(50, dtype=np.int64), loc,
-        np.array([0, 50], np.int32), np.array([0], np.int32), eng._rows[req.uid][None])
+        b.input_ids, b.positions, b.write_loc, b.cu_seqlens_q, b.prefix_lens, b.block_table)
     meta = AttentionMetadata(BatchPhase.PREFILL, write_loc=loc_d, cu_seqlens_q=cu_d,
                              prefix_lens=pre_d, block_table=tab_d,
                              host_cu_seqlens_q=[0, 50], host_prefix_lens=[0])
