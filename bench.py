@@ -418,6 +418,31 @@ def prefill_sections(dev, reps: int, cpu: bool = True) -> dict:
             "kind": "port", "sample": f"2 of 16 requests ({sb[-1]} extend tokens over "
                                       f"{int(pref[rows].sum())} cached), torch-CPU fp32 "
                                       "restatement, median of 3"}
+    del plan
+    # A chunked-prefill continuation, which the configs above do not cover: one request with
+    # an 8,192-token cached prefix and 64 new tokens (Hq32/Hkv8, page 16, random pages). Only
+    # 8 items for 256 CUs, so the plan splits them along their keys and merges the chunks.
+    page, prefix, extend = 16, 8192, 64
+    n_pages = (prefix + extend + page - 1) // page
+    perm = (torch.randperm(n_pages, generator=g) + 1).to(torch.int32)
+    kc = torch.randn(n_pages + 1, page, 8, 128, generator=gd, device=dev, dtype=torch.bfloat16)
+    vc = torch.randn(n_pages + 1, page, 8, 128, generator=gd, device=dev, dtype=torch.bfloat16)
+    q = torch.randn(extend, 32, 128, generator=gd, device=dev, dtype=torch.bfloat16)
+    meta = AttentionMetadata(BatchPhase.PREFILL,
+                             cu_seqlens_q=torch.tensor([0, extend], dtype=torch.int32, device=dev),
+                             prefix_lens=torch.tensor([prefix], dtype=torch.int32, device=dev),
+                             block_table=perm.view(1, -1).to(dev))
+    plan = prepare_prefill_plan(None, meta, PrefillMetadata([0, extend], [prefix]), spec, page)
+    o = torch.empty_like(q)
+    for _ in range(PREFILL_WARMUP):
+        run_prefill(plan, q, kc, vc, o)
+    ms = _event_time_ms(lambda: run_prefill(plan, q, kc, vc, o), reps)
+    flops = 4 * 32 * 128 * (extend * prefix + extend * (extend + 1) // 2)
+    info = plan.info()
+    out["prefill_paged_long_prefix"] = {
+        "us": round(ms * 1e3, 2), "flops": flops, "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2),
+        "work_items": info["num_items"], "split_items": info["split_items"],
+        "shape": f"1 request, prefix {prefix}, extend {extend}, Hq32/Hkv8, page {page}"}
     return out
 
 

@@ -181,8 +181,9 @@ void mi355x_prefill_plan_drop(void* plan);
 /* Workspace (re)allocations made by a prefill plan so far. */
 uint64_t mi355x_prefill_workspace_allocations(const void* plan);
 
-/* Plan facts: out6 = {batch, total_q, paged, num_items, total_pages, 0}.
- * Introspection; no reference counterpart. */
+/* Plan facts: out6 = {batch, total_q, paged, num_items, total_pages, split_items}:
+ * num_items counts launched work items (chunks included), split_items the items cut
+ * along their keys and merged by a second launch. Introspection; no reference counterpart. */
 const char* mi355x_prefill_plan_info(const void* plan, int64_t* out6);
 
 /* Blocking copy of kv_indptr (batch+1) and, for paged plans, indices
@@ -193,7 +194,9 @@ const char* mi355x_prefill_plan_read(const void* plan, int32_t* kv_indptr, int32
 /* Host-only prefill work list: 4 ints per item {request, q_begin, kv_head,
  * head_group}, longest causal horizon first. work may be NULL to count.
  * Returns the item count or -1. Stands in for FlashInfer's PrefillPlan
- * tiling (flashinfer_plan_run.cu:243-274). */
+ * tiling (flashinfer_plan_run.cu:243-274). mi355x_prefill_prepare further cuts
+ * items along their keys when the batch is too small to fill the device (when the
+ * longest item exceeds twice the mean per-CU share of 64-key tiles). */
 int64_t mi355x_prefill_schedule(const int32_t* q_host, const int32_t* prefix_host, int64_t batch,
                                 int64_t num_q_heads, int64_t num_kv_heads, int32_t* work,
                                 int64_t capacity);

@@ -21,6 +21,9 @@
 // K/V tiles stream through a 4-deep LDS ring filled by direct global -> LDS copies (one
 // barrier per tile); the g q heads that share a kv head are processed by the same
 // workgroup so each K/V byte is fetched once per tile.
+// Split-KV: when a batch has too few items to fill the device (a long prefix under few
+// queries), the plan cuts items into chunks of key tiles; each chunk writes a normalised
+// fp32 partial and its log2-sum-exp, and prefill_merge_kernel combines them.
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -81,7 +84,10 @@ struct PrefillArgs {
   uint16_t* out;
   int64_t o_sn, o_sh;
   const ReqInfo* reqs;
-  const int4* work;  // {request, q_begin, kv_head, head_group}
+  const int4* work;    // {request, q_begin, kv_head, head_group}
+  const int4* ranges;  // per item {first tile, end tile, partial record or -1, 0}
+  float* part_o;       // split items: [record][8 slots][32 queries][128] normalised O
+  float* part_lse;     // split items: [record][8 slots][32 queries] log2-sum-exp
   const int32_t* indices;
   int32_t num_items, num_q_heads, num_kv_heads, page_size;
   float scale_log2;
@@ -159,6 +165,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
 
   const int4 w = a.work[blockIdx.x];
   if (w.x < 0) return;  // padding slot of the XCD-ordered work list
+  const int4 range = a.ranges[blockIdx.x];
   const ReqInfo rq = a.reqs[w.x];
   const int q_begin = w.y;
   const int kvh = w.z;
@@ -175,6 +182,11 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
   const int q_hi = min(q_begin + kBQ, rq.q_len);
   const int keys_needed = min(kv_len, rq.prefix + q_hi);
   const int n_tiles = (keys_needed + kTileK - 1) / kTileK;
+  // This item's key tiles: all of them, or one chunk of a split item, whose normalised
+  // partial result goes to a partial record for the merge launch.
+  const int t_begin = range.x;
+  const int nt = min(range.y, n_tiles) - t_begin;
+  const int pslot = range.z;
   const bool wave_active = wq0 < rq.q_len;
   const int wave_last_key = rq.prefix + min(wq0 + kQPerWave, rq.q_len) - 1;
 
@@ -330,7 +342,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
   // rescale, P^T = 2^(s scale - m), O^T += V^T P^T.
   // One 64-key tile per step: S^T = K Q^T - m (two 32-key blocks), mask and row max,
   // lazy rescale, P^T = 2^(S^T), O^T += V^T P^T.
-  auto compute = [&](int t, int stage) {
+  auto compute = [&](int t, int stage, bool first) {
     const int k0 = t * kTileK;
     if (!(wave_active && k0 <= wave_last_key)) return;
     const uint8_t* sb = lds + stage * kStageBytes;
@@ -380,9 +392,11 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
     }
     // Lazy rescale: m moves on the first tile (to the row max) and afterwards only when
     // some row's max exceeds it by more than 8, so p = 2^(s - m) <= 2^8 and O / l are
-    // rescaled rarely. Every tile starts at key 0, which each query sees, so mx is finite.
-    if (t == 0 || __any(mx > 8.f)) {
-      const float shift = t == 0 ? mx : fmaxf(mx, 0.f);
+    // rescaled rarely. The first tile of a whole item holds key 0, which each query sees,
+    // so mx is finite there; the first tile of a later chunk can lie wholly past a query's
+    // horizon (mx = -inf), and that row then keeps m = 0 until a key reaches it.
+    if (first || __any(mx > 8.f)) {
+      const float shift = first ? (mx == -INFINITY ? 0.f : mx) : fmaxf(mx, 0.f);
       const float alpha = __builtin_amdgcn_exp2f(-shift);
       m += shift;
       l *= alpha;
@@ -420,20 +434,38 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
   };
 
   if constexpr (PAGED) {
-    if (fast_pages) load_ids(0);
+    if (fast_pages) load_ids(t_begin);
   }
 #pragma unroll
   for (int st = 0; st < kAhead; ++st)
-    if (st < n_tiles) issue(st, st);
-  for (int t = 0; t < n_tiles; ++t) {
-    wait_tiles_ahead<kCopiesPerTile, kAhead - 1>(min(kAhead - 1, n_tiles - 1 - t));
+    if (st < nt) issue(t_begin + st, st);
+  for (int u = 0; u < nt; ++u) {
+    wait_tiles_ahead<kCopiesPerTile, kAhead - 1>(min(kAhead - 1, nt - 1 - u));
     __syncthreads();
-    if (t + kAhead < n_tiles) issue(t + kAhead, (t + kAhead) % STAGES);
-    compute(t, t % STAGES);
+    if (u + kAhead < nt) issue(t_begin + u + kAhead, (u + kAhead) % STAGES);
+    compute(t_begin + u, u % STAGES, u == 0);
   }
 
   if (!wave_active || my_q >= rq.q_len) return;
-  const float inv = 1.f / (l + __shfl_xor(l, 32));
+  const float row_sum = l + __shfl_xor(l, 32);
+  if (pslot >= 0) {
+    // Chunk of a split item: O / l and m + log2 l (or 0 and -inf when no key of the
+    // chunk reaches this query) for the merge launch.
+    const float inv = row_sum > 0.f ? 1.f / row_sum : 0.f;
+    const int64_t rec = (static_cast<int64_t>(pslot) * NW + slot_id) * kQPerWave + col;
+    float* po = a.part_o + rec * kD;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+        *reinterpret_cast<float4*>(po + 32 * db + 8 * g4 + 4 * half) =
+            make_float4(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv, o[db][4 * g4 + 2] * inv,
+                        o[db][4 * g4 + 3] * inv);
+    if (half == 0)
+      a.part_lse[rec] = row_sum > 0.f ? m + __builtin_amdgcn_logf(row_sum) : -INFINITY;
+    return;
+  }
+  const float inv = 1.f / row_sum;
   uint16_t* op = a.out + static_cast<int64_t>(rq.q_start + my_q) * a.o_sn + qh * a.o_sh;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -444,6 +476,65 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
                                    pack2<DT>(o[db][4 * g4 + 2] * inv, o[db][4 * g4 + 3] * inv));
       *reinterpret_cast<uint2*>(op + d) = val;
     }
+}
+
+// Merge of split items: one workgroup per (split item, wave slot), 8 threads per query row
+// of the slot, 16 dims per thread. Chunks combine by their log2-sum-exp (a chunk with
+// lse = -inf adds nothing); every query sees key 0, so at least one chunk is finite.
+// groups: per split item {request, q_begin, kv_head, head_group}, {first record, count}.
+template <int DT>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a, const int4* groups,
+                                                            int waves_per_head, int hpb) {
+  const int gi = blockIdx.x;
+  const int slot = blockIdx.y;
+  const int4 w = groups[2 * gi];
+  const int4 cnt = groups[2 * gi + 1];
+  const ReqInfo rq = a.reqs[w.x];
+  const int group = a.num_q_heads / a.num_kv_heads;
+  const int qh = w.z * group + w.w * hpb + slot / waves_per_head;
+  const int q = threadIdx.x >> 3;
+  const int part = threadIdx.x & 7;
+  const int my_q = w.y + (slot % waves_per_head) * kQPerWave + q;
+  if (my_q >= rq.q_len) return;
+  float mx = -INFINITY, den = 0.f, acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  for (int c = 0; c < cnt.y; ++c) {
+    const int64_t rec = (static_cast<int64_t>(cnt.x + c) * kWaves + slot) * kQPerWave + q;
+    const float lse = a.part_lse[rec];
+    if (lse == -INFINITY) continue;
+    const float* po = a.part_o + rec * kD + 16 * part;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(po + i);
+      v[i] = x.x;
+      v[i + 1] = x.y;
+      v[i + 2] = x.z;
+      v[i + 3] = x.w;
+    }
+    const float m_new = fmaxf(mx, lse);
+    const float corr = __builtin_amdgcn_exp2f(mx - m_new);
+    const float wgt = __builtin_amdgcn_exp2f(lse - m_new);
+    den = den * corr + wgt;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = fmaf(wgt, v[i], acc[i] * corr);
+    mx = m_new;
+  }
+  const float inv = 1.f / den;
+  uint16_t* op = a.out + static_cast<int64_t>(rq.q_start + my_q) * a.o_sn + qh * a.o_sh +
+                 16 * part;
+  uint4 lo, hi;
+  lo.x = pack2<DT>(acc[0] * inv, acc[1] * inv);
+  lo.y = pack2<DT>(acc[2] * inv, acc[3] * inv);
+  lo.z = pack2<DT>(acc[4] * inv, acc[5] * inv);
+  lo.w = pack2<DT>(acc[6] * inv, acc[7] * inv);
+  hi.x = pack2<DT>(acc[8] * inv, acc[9] * inv);
+  hi.y = pack2<DT>(acc[10] * inv, acc[11] * inv);
+  hi.z = pack2<DT>(acc[12] * inv, acc[13] * inv);
+  hi.w = pack2<DT>(acc[14] * inv, acc[15] * inv);
+  *reinterpret_cast<uint4*>(op) = lo;
+  *reinterpret_cast<uint4*>(op + 8) = hi;
 }
 
 __global__ __launch_bounds__(256) void pack_prefill_pages(const int32_t* __restrict__ table,
@@ -498,9 +589,13 @@ struct PrefillPlan {
   int64_t num_q_heads = 0, num_kv_heads = 0, page_size = 0, dtype = 0;
   int64_t batch = 0, total_q = 0, num_items = 0, total_pages = 0;
   bool paged = false;
-  // Device int32 workspace: [req info 4*B][work 4*items][kv_indptr B+1][last_len B]
-  int64_t o_work = 0, o_indptr = 0, o_last = 0;
-  Buffer ints, indices, staging;
+  int64_t cus = 0;          // compute units of the plan's device
+  int64_t num_groups = 0;   // items split along the keys (merged by a second launch)
+  int64_t num_records = 0;  // partial records (chunks of split items)
+  // Device int32 workspace: [req info 4*B][work 4*items][ranges 4*items][kv_indptr B+1]
+  // [last_len B][groups 8*num_groups]
+  int64_t o_work = 0, o_ranges = 0, o_indptr = 0, o_last = 0, o_groups = 0;
+  Buffer ints, indices, staging, part_o, part_lse;
   hipEvent_t upload_done = nullptr;
   uint64_t allocations = 0;
   PrefillPlan() { staging.pinned = true; }
@@ -562,6 +657,80 @@ extern "C" int64_t mi355x_prefill_schedule(const int32_t* q_host, const int32_t*
   }
   return n;
 }
+
+namespace mi355x {
+namespace {
+constexpr int64_t kMinChunkTiles = 8;  // keys of a split chunk: at least 8 tiles (512)
+
+// Splits the items of a work list along their keys when the batch is too small to fill the
+// chip (the reference's prefill plan splits KV the same way for low parallelism,
+// flashinfer_plan_run.cu:243-274,312-316): when the longest item holds more than twice the
+// mean per-CU share of tiles, every item longer than max(8, that share) becomes
+// ceil(tiles / chunk) chunks of near-equal length. Unsplit items keep range {0, tiles, -1};
+// chunk j of split item g gets {first, end, record} with records consecutive per item.
+// Output order: longest chunk or item first.
+struct SplitPlan {
+  std::vector<int32_t> work, ranges, groups;  // 4, 4 and 8 ints per entry
+  int64_t records = 0;
+};
+SplitPlan split_items(const std::vector<int32_t>& base, const int32_t* q_host,
+                      const int32_t* prefix_host, int64_t num_q_heads, int64_t num_kv_heads,
+                      int64_t cus) {
+  const int64_t n = static_cast<int64_t>(base.size() / 4);
+  const int hpb = heads_per_block(num_q_heads / num_kv_heads);
+  const int64_t bq = kQPerWave * (kWaves / hpb);
+  std::vector<int64_t> tiles(n);
+  int64_t total = 0, longest = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const int r = base[4 * i];
+    const int64_t q_len = q_host[r + 1] - q_host[r];
+    const int64_t horizon = prefix_host[r] + std::min<int64_t>(base[4 * i + 1] + bq, q_len);
+    tiles[i] = (horizon + kTileK - 1) / kTileK;
+    total += tiles[i];
+    longest = std::max(longest, tiles[i]);
+  }
+  const int64_t share = (total + cus - 1) / std::max<int64_t>(cus, 1);
+  // MI355X_PREFILL_SPLIT=0 turns splitting off (tuning knob, read once).
+  static const bool enabled = [] {
+    const char* env = std::getenv("MI355X_PREFILL_SPLIT");
+    return !(env && std::strcmp(env, "0") == 0);
+  }();
+  const bool split = enabled && longest > 2 * share && longest > 2 * kMinChunkTiles;
+  const int64_t chunk = std::max(kMinChunkTiles, share);
+  struct Entry {
+    int64_t cost;
+    int64_t item, first, end, record;
+  };
+  std::vector<Entry> entries;
+  SplitPlan out;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t k = split && tiles[i] > chunk ? (tiles[i] + chunk - 1) / chunk : 1;
+    if (k == 1) {
+      entries.push_back({tiles[i], i, 0, tiles[i], -1});
+      continue;
+    }
+    const int64_t group = static_cast<int64_t>(out.groups.size() / 8);
+    out.groups.insert(out.groups.end(), base.begin() + 4 * i, base.begin() + 4 * i + 4);
+    out.groups.insert(out.groups.end(), {static_cast<int32_t>(out.records),
+                                         static_cast<int32_t>(k), 0, 0});
+    (void)group;
+    for (int64_t j = 0; j < k; ++j) {
+      const int64_t first = tiles[i] * j / k, end = tiles[i] * (j + 1) / k;
+      entries.push_back({end - first, i, first, end, out.records++});
+    }
+  }
+  std::stable_sort(entries.begin(), entries.end(),
+                   [](const Entry& x, const Entry& y) { return x.cost > y.cost; });
+  for (const Entry& e : entries) {
+    out.work.insert(out.work.end(), base.begin() + 4 * e.item, base.begin() + 4 * e.item + 4);
+    out.ranges.insert(out.ranges.end(), {static_cast<int32_t>(e.first),
+                                         static_cast<int32_t>(e.end),
+                                         static_cast<int32_t>(e.record), 0});
+  }
+  return out;
+}
+}  // namespace
+}  // namespace mi355x
 
 extern "C" void* mi355x_prefill_prepare(void* existing, const int32_t* q_indptr,
                                         const int32_t* block_table, int64_t batch,
@@ -632,23 +801,50 @@ extern "C" void* mi355x_prefill_prepare(void* existing, const int32_t* q_indptr,
         return nullptr;
       }
     }
-    const int64_t n_items =
+    const int64_t n_base =
         mi355x_prefill_schedule(q_host, prefix_host, batch, num_q_heads, num_kv_heads, nullptr, 0);
-    if (n_items <= 0 || n_items > std::numeric_limits<int32_t>::max()) {
+    if (n_base <= 0 || n_base > std::numeric_limits<int32_t>::max() / 64) {
+      set_error("prefill work list is empty or too large");
+      return nullptr;
+    }
+    if (!plan->cus) {
+      int cus = 0;
+      st = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+      if (st != hipSuccess || cus <= 0) {
+        hip_error(st, "hipDeviceGetAttribute");
+        return nullptr;
+      }
+      plan->cus = cus;
+    }
+    std::vector<int32_t> base(4 * n_base);
+    mi355x_prefill_schedule(q_host, prefix_host, batch, num_q_heads, num_kv_heads, base.data(),
+                            n_base);
+    const SplitPlan sp =
+        split_items(base, q_host, prefix_host, num_q_heads, num_kv_heads, plan->cus);
+    const int64_t n_items = static_cast<int64_t>(sp.work.size() / 4);
+    const int64_t n_groups = static_cast<int64_t>(sp.groups.size() / 8);
+    if (n_items > std::numeric_limits<int32_t>::max() / 64) {
       set_error("prefill work list is empty or too large");
       return nullptr;
     }
     const int64_t o_work = 4 * batch;
-    const int64_t o_indptr = o_work + 4 * n_items;
+    const int64_t o_ranges = o_work + 4 * n_items;
+    const int64_t o_indptr = o_ranges + 4 * n_items;
     const int64_t o_last = o_indptr + batch + 1;
-    const int64_t total_ints = o_last + batch;
+    const int64_t o_groups = (o_last + batch + 3) / 4 * 4;  // int4-aligned
+    const int64_t total_ints = o_groups + 8 * n_groups;
     st = hipEventSynchronize(plan->upload_done);
     if (st != hipSuccess) {
       hip_error(st, "prefill upload fence");
       return nullptr;
     }
+    const size_t rec_bytes = static_cast<size_t>(sp.records) * kWaves * kQPerWave * 4;
     if ((st = plan->ints.reserve(total_ints * 4, plan->allocations)) != hipSuccess ||
-        (st = plan->staging.reserve(total_ints * 4, plan->allocations)) != hipSuccess) {
+        (st = plan->staging.reserve(total_ints * 4, plan->allocations)) != hipSuccess ||
+        (sp.records && (st = plan->part_o.reserve(rec_bytes * kD, plan->allocations)) !=
+                           hipSuccess) ||
+        (sp.records && (st = plan->part_lse.reserve(rec_bytes, plan->allocations)) !=
+                           hipSuccess)) {
       hip_error(st, "prefill workspace allocation");
       return nullptr;
     }
@@ -675,8 +871,9 @@ extern "C" void* mi355x_prefill_prepare(void* existing, const int32_t* q_indptr,
         host[o_last + r] = 0;
       }
     }
-    mi355x_prefill_schedule(q_host, prefix_host, batch, num_q_heads, num_kv_heads,
-                            host + o_work, n_items);
+    std::memcpy(host + o_work, sp.work.data(), sp.work.size() * 4);
+    std::memcpy(host + o_ranges, sp.ranges.data(), sp.ranges.size() * 4);
+    if (n_groups) std::memcpy(host + o_groups, sp.groups.data(), sp.groups.size() * 4);
     st = hipMemcpyAsync(plan->ints.ptr, host, total_ints * 4, hipMemcpyHostToDevice, s);
     if (st != hipSuccess) {
       hip_error(st, "prefill metadata upload");
@@ -701,11 +898,15 @@ extern "C" void* mi355x_prefill_prepare(void* existing, const int32_t* q_indptr,
     plan->batch = batch;
     plan->total_q = q_host[batch];
     plan->num_items = n_items;
+    plan->num_groups = n_groups;
+    plan->num_records = sp.records;
     plan->total_pages = total_pages;
     plan->paged = paged;
     plan->o_work = o_work;
+    plan->o_ranges = o_ranges;
     plan->o_indptr = o_indptr;
     plan->o_last = o_last;
+    plan->o_groups = o_groups;
     created.release();
     return plan;
   } catch (const std::exception& e) {
@@ -720,7 +921,7 @@ extern "C" uint64_t mi355x_prefill_workspace_allocations(const void* plan) {
   return plan ? static_cast<const PrefillPlan*>(plan)->allocations : 0;
 }
 
-// Plan facts: out6 = {batch, total_q, paged, num_items, total_pages, 0}.
+// Plan facts: out6 = {batch, total_q, paged, num_items, total_pages, items split along keys}.
 extern "C" const char* mi355x_prefill_plan_info(const void* plan, int64_t* out6) {
   if (!plan || !out6) return set_error("mi355x_prefill_plan_info: null argument");
   const auto* p = static_cast<const PrefillPlan*>(plan);
@@ -729,7 +930,7 @@ extern "C" const char* mi355x_prefill_plan_info(const void* plan, int64_t* out6)
   out6[2] = p->paged ? 1 : 0;
   out6[3] = p->num_items;
   out6[4] = p->total_pages;
-  out6[5] = 0;
+  out6[5] = p->num_groups;
   return nullptr;
 }
 
@@ -765,11 +966,15 @@ void launch_prefill(const PrefillArgs& a, bool paged, hipStream_t s) {
     prefill_kernel<DT, HPB, false><<<grid, block, 0, s>>>(a);
 }
 template <int DT>
-void launch_dt(const PrefillArgs& a, int hpb, bool paged, hipStream_t s) {
+void launch_dt(const PrefillArgs& a, int hpb, bool paged, const int4* groups,
+               int64_t num_groups, hipStream_t s) {
   if (hpb == 1) launch_prefill<DT, 1>(a, paged, s);
   else if (hpb == 2) launch_prefill<DT, 2>(a, paged, s);
   else if (hpb == 4) launch_prefill<DT, 4>(a, paged, s);
   else launch_prefill<DT, 8>(a, paged, s);
+  if (num_groups)
+    prefill_merge_kernel<DT><<<dim3(static_cast<uint32_t>(num_groups), kWaves), dim3(256), 0,
+                               s>>>(a, groups, kWaves / hpb, hpb);
 }
 }  // namespace
 }  // namespace mi355x
@@ -806,6 +1011,9 @@ extern "C" const char* mi355x_prefill_run(const void* plan_ptr, const void* q, i
   const int32_t* ints = static_cast<const int32_t*>(p.ints.ptr);
   a.reqs = reinterpret_cast<const ReqInfo*>(ints);
   a.work = reinterpret_cast<const int4*>(ints + p.o_work);
+  a.ranges = reinterpret_cast<const int4*>(ints + p.o_ranges);
+  a.part_o = static_cast<float*>(p.part_o.ptr);
+  a.part_lse = static_cast<float*>(p.part_lse.ptr);
   a.indices = static_cast<const int32_t*>(p.indices.ptr);
   a.num_items = static_cast<int32_t>(p.num_items);
   a.num_q_heads = static_cast<int32_t>(num_q_heads);
@@ -814,9 +1022,10 @@ extern "C" const char* mi355x_prefill_run(const void* plan_ptr, const void* q, i
   a.scale_log2 = (1.0f / std::sqrt(static_cast<float>(kD))) * kLog2e;
   const int hpb = heads_per_block(num_q_heads / num_kv_heads);
   auto s = static_cast<hipStream_t>(stream);
+  const int4* groups = reinterpret_cast<const int4*>(ints + p.o_groups);
   if (dtype == 0)
-    launch_dt<0>(a, hpb, p.paged, s);
+    launch_dt<0>(a, hpb, p.paged, groups, p.num_groups, s);
   else
-    launch_dt<1>(a, hpb, p.paged, s);
+    launch_dt<1>(a, hpb, p.paged, groups, p.num_groups, s);
   return launch_status("prefill_kernel");
 }

@@ -28,7 +28,7 @@ class PrefillPlan:
     def info(self) -> dict[str, int]:
         buf = (ctypes.c_int64 * 6)()
         check(lib().mi355x_prefill_plan_info(self.handle, buf), "prefill plan info")
-        keys = ("batch", "total_q", "paged", "num_items", "total_pages")
+        keys = ("batch", "total_q", "paged", "num_items", "total_pages", "split_items")
         return dict(zip(keys, list(buf)))
 
     def allocations(self) -> int:

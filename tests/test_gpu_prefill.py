@@ -122,6 +122,7 @@ def test_config3_ragged_shape(gpu):
     attn = make(gpu, 16, 8, 16, torch.bfloat16)
     table = torch.zeros(8, 2048 // 16, dtype=torch.int32, device=gpu)
     batch = attn.prepare(meta_for(gpu, bounds, [0] * 8, table), n)
+    assert batch.plan.plan.info()["split_items"] == 0  # enough items to fill the device
     out = batch.forward(q, k, v, BaseAttention())
     want = oatt.prefill_ragged(f32(q), f32(k), f32(v), bounds)
     assert_close(f32(out).reshape(want.shape), want, "config3")
@@ -155,7 +156,7 @@ def test_config4_paged_shape_sampled_rows(gpu):
     cache.bind_kv_cache(kc, vc)
     tdev = torch.from_numpy(table).to(gpu)
     batch = attn.prepare(meta_for(gpu, bounds, pref.tolist(), tdev), n)
-    assert batch.plan.plan.paged
+    assert batch.plan.plan.paged and batch.plan.plan.info()["split_items"] == 0
     out = f32(batch.forward(q, q, q, cache)).reshape(n, 32, 128)
     kcf, vcf, qf = f32(kc), f32(vc), f32(q)
     flat_k = kcf.reshape(-1, 8, 128)
@@ -245,3 +246,57 @@ def test_paged_small_prefixes_and_tiny_extends(gpu, seed):
             want = oatt.attention_against_cache(qf[bounds[r] + i: bounds[r] + i + 1],
                                                 flat_k[slots], flat_v[slots], horizon - 1, 32, 8)
             assert_close(out[bounds[r] + i], want[0], f"seed={seed} req={r} row={i}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_long_prefix_few_queries_is_split_along_keys(gpu, dtype):
+    """A chunked-prefill continuation: one request with an 8,192-token cached prefix (random
+    page permutation) and 64 new tokens, beside a 3-token request, Hq32/Hkv8, page 16. That
+    is 16 work items for 256 CUs, so the plan cuts the long items along their keys and a
+    merge launch combines the chunks (the reference's split-KV prefill plan,
+    flashinfer_plan_run.cu:312-316); every row checked against the oracle."""
+    rng = np.random.default_rng(21)
+    g = torch.Generator().manual_seed(21)
+    page = 16
+    pref = np.array([8192, 5])
+    ext = np.array([64, 3])
+    bounds = [0] + np.cumsum(ext).tolist()
+    pages_per = (pref + ext + page - 1) // page
+    pool = int(pages_per.sum()) + 1
+    perm = rng.permutation(pool - 1) + 1
+    table = np.zeros((2, int(pages_per.max())), np.int32)
+    table[0, : pages_per[0]] = perm[: pages_per[0]]
+    table[1, : pages_per[1]] = perm[pages_per[0]: pages_per[0] + pages_per[1]]
+    kc = randn((pool, page, 8, 128), g, dtype, gpu)
+    vc = randn((pool, page, 8, 128), g, dtype, gpu)
+    n = bounds[-1]
+    q = randn((n, 32, 128), g, dtype, gpu)
+    attn = make(gpu, 32, 8, page, dtype)
+    cache = BaseAttention()
+    cache.bind_kv_cache(kc, vc)
+    batch = attn.prepare(meta_for(gpu, bounds, pref.tolist(), torch.from_numpy(table).to(gpu)), n)
+    info = batch.plan.plan.info()
+    assert info["split_items"] == 8 and info["num_items"] > 64, info
+    out = f32(batch.forward(q, q, q, cache)).reshape(n, 32, 128)
+    want = oatt.prefill_with_cache(f32(q), f32(kc), f32(vc), table, bounds, pref, page)
+    for r in range(2):
+        assert_close(out[bounds[r]:bounds[r + 1]], want[bounds[r]:bounds[r + 1]], f"req={r}")
+
+
+@pytest.mark.parametrize("hq,hkv", [(2, 2), (4, 2), (8, 1)])
+def test_single_long_sequence_is_split_along_keys(gpu, hq, hkv):
+    """One 2,000-token ragged sequence with few heads (query blocks of 256, 128 and 32
+    queries): too few items for the device, so long items are split along their keys and
+    merged; every row checked."""
+    g = torch.Generator().manual_seed(hq * 10 + hkv)
+    bounds = [0, 2000]
+    q = randn((2000, hq, 128), g, torch.bfloat16, gpu)
+    k = randn((2000, hkv, 128), g, torch.bfloat16, gpu)
+    v = randn((2000, hkv, 128), g, torch.bfloat16, gpu)
+    attn = make(gpu, hq, hkv, 16, torch.bfloat16)
+    table = torch.zeros(1, 128, dtype=torch.int32, device=gpu)
+    batch = attn.prepare(meta_for(gpu, bounds, [0], table), 2000)
+    assert batch.plan.plan.info()["split_items"] > 0
+    out = batch.forward(q, k, v, BaseAttention())
+    want = oatt.prefill_ragged(f32(q), f32(k), f32(v), bounds)
+    assert_close(f32(out).reshape(want.shape), want, f"hq={hq} hkv={hkv}")
