@@ -709,11 +709,9 @@ SplitPlan split_items(const std::vector<int32_t>& base, const int32_t* q_host,
       entries.push_back({tiles[i], i, 0, tiles[i], -1});
       continue;
     }
-    const int64_t group = static_cast<int64_t>(out.groups.size() / 8);
     out.groups.insert(out.groups.end(), base.begin() + 4 * i, base.begin() + 4 * i + 4);
     out.groups.insert(out.groups.end(), {static_cast<int32_t>(out.records),
                                          static_cast<int32_t>(k), 0, 0});
-    (void)group;
     for (int64_t j = 0; j < k; ++j) {
       const int64_t first = tiles[i] * j / k, end = tiles[i] * (j + 1) / k;
       entries.push_back({end - first, i, first, end, out.records++});
