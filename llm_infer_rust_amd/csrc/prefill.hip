@@ -580,7 +580,17 @@ struct Buffer {
 
 // q heads per workgroup: all g heads of a kv head when g <= 8 waves, so each K/V tile
 // is fetched once for the whole group.
-int heads_per_block(int64_t group) { return static_cast<int>(std::min<int64_t>(group, kWaves)); }
+int heads_per_block(int64_t group) {
+  // MI355X_PREFILL_HPB (1, 2, 4 or 8, at most the group) overrides the default of every
+  // q head of the group in one workgroup (tuning knob, read once).
+  static const int forced = [] {
+    const char* env = std::getenv("MI355X_PREFILL_HPB");
+    const int v = env ? std::atoi(env) : 0;
+    return (v == 1 || v == 2 || v == 4 || v == 8) ? v : 0;
+  }();
+  if (forced && forced <= group && group % forced == 0) return forced;
+  return static_cast<int>(std::min<int64_t>(group, kWaves));
+}
 
 }  // namespace
 
