@@ -446,36 +446,53 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
     compute(t_begin + u, u % STAGES, u == 0);
   }
 
-  if (!wave_active || my_q >= rq.q_len) return;
+  if (!wave_active) return;
   const float row_sum = l + __shfl_xor(l, 32);
   if (pslot >= 0) {
     // Chunk of a split item: O / l and m + log2 l (or 0 and -inf when no key of the
-    // chunk reaches this query) for the merge launch.
+    // chunk reaches this query) for the merge launch. The record keeps the lanes' own
+    // order (float4 f = (4 db + g4) * 64 + lane), so each store covers 1 KB contiguously.
+    if (my_q >= rq.q_len) return;
     const float inv = row_sum > 0.f ? 1.f / row_sum : 0.f;
-    const int64_t rec = (static_cast<int64_t>(pslot) * NW + slot_id) * kQPerWave + col;
-    float* po = a.part_o + rec * kD;
+    const int64_t rec = static_cast<int64_t>(pslot) * NW + slot_id;
+    float* po = a.part_o + rec * (kQPerWave * kD);
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4)
-        *reinterpret_cast<float4*>(po + 32 * db + 8 * g4 + 4 * half) =
+        *reinterpret_cast<float4*>(po + ((4 * db + g4) * 64 + lane) * 4) =
             make_float4(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv, o[db][4 * g4 + 2] * inv,
                         o[db][4 * g4 + 3] * inv);
     if (half == 0)
-      a.part_lse[rec] = row_sum > 0.f ? m + __builtin_amdgcn_logf(row_sum) : -INFINITY;
+      a.part_lse[rec * kQPerWave + col] =
+          row_sum > 0.f ? m + __builtin_amdgcn_logf(row_sum) : -INFINITY;
     return;
   }
+  // The wave's 32 x 128 output tile goes out as whole 256-byte rows: written to an LDS
+  // region no wave reads any more (a stage other than the last tile's; waves 0-3 and 4-7
+  // take two different stages, 8 KB each, 16-byte chunks XOR-swizzled by row so both the
+  // column writes and the row reads are conflict-free), then read back row-major.
+  // (Lane-order stores of 16 bytes per query row cost ~4.8 us per item at config 3.)
   const float inv = 1.f / row_sum;
-  uint16_t* op = a.out + static_cast<int64_t>(rq.q_start + my_q) * a.o_sn + qh * a.o_sh;
+  uint8_t* tile = lds + ((nt + (wave >> 2)) % STAGES) * kStageBytes + (wave & 3) * 8192;
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      const int d = 32 * db + 8 * g4 + 4 * half;
-      const uint2 val = make_uint2(pack2<DT>(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv),
-                                   pack2<DT>(o[db][4 * g4 + 2] * inv, o[db][4 * g4 + 3] * inv));
-      *reinterpret_cast<uint2*>(op + d) = val;
+      const int chunk = (4 * db + g4) ^ (col & 15);
+      *reinterpret_cast<uint2*>(tile + col * 256 + chunk * 16 + half * 8) =
+          make_uint2(pack2<DT>(o[db][4 * g4] * inv, o[db][4 * g4 + 1] * inv),
+                     pack2<DT>(o[db][4 * g4 + 2] * inv, o[db][4 * g4 + 3] * inv));
     }
+  const int c16 = lane & 15;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int row = 4 * j + (lane >> 4);
+    const uint4 val = *reinterpret_cast<const uint4*>(tile + row * 256 + ((c16 ^ (row & 15)) * 16));
+    if (wq0 + row < rq.q_len)
+      *reinterpret_cast<uint4*>(a.out + static_cast<int64_t>(rq.q_start + wq0 + row) * a.o_sn +
+                                qh * a.o_sh + c16 * 8) = val;
+  }
 }
 
 // Merge of split items: one workgroup per (split item, wave slot), 8 threads per query row
@@ -500,19 +517,24 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a, const
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.f;
   for (int c = 0; c < cnt.y; ++c) {
-    const int64_t rec = (static_cast<int64_t>(cnt.x + c) * kWaves + slot) * kQPerWave + q;
-    const float lse = a.part_lse[rec];
+    const int64_t rec = static_cast<int64_t>(cnt.x + c) * kWaves + slot;
+    const float lse = a.part_lse[rec * kQPerWave + q];
     if (lse == -INFINITY) continue;
-    const float* po = a.part_o + rec * kD + 16 * part;
+    // Dims 16 part + 8 j + 4 h + i sit in float4 ((4 db + g4) * 64 + lane) of the record,
+    // db = part / 2, g4 = 2 (part % 2) + j, lane = q + 32 h (the main kernel's lane order).
+    const float* po = a.part_o + rec * (kQPerWave * kD);
     float v[16];
 #pragma unroll
-    for (int i = 0; i < 16; i += 4) {
-      const float4 x = *reinterpret_cast<const float4*>(po + i);
-      v[i] = x.x;
-      v[i + 1] = x.y;
-      v[i + 2] = x.z;
-      v[i + 3] = x.w;
-    }
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int f = (4 * (part >> 1) + 2 * (part & 1) + j) * 64 + q + 32 * h;
+        const float4 x = *reinterpret_cast<const float4*>(po + f * 4);
+        v[8 * j + 4 * h] = x.x;
+        v[8 * j + 4 * h + 1] = x.y;
+        v[8 * j + 4 * h + 2] = x.z;
+        v[8 * j + 4 * h + 3] = x.w;
+      }
     const float m_new = fmaxf(mx, lse);
     const float corr = __builtin_amdgcn_exp2f(mx - m_new);
     const float wgt = __builtin_amdgcn_exp2f(lse - m_new);
