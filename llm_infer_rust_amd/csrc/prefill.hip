@@ -495,68 +495,64 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
   }
 }
 
-// Merge of split items: one workgroup per (split item, wave slot), 8 threads per query row
-// of the slot, 16 dims per thread. Chunks combine by their log2-sum-exp (a chunk with
-// lse = -inf adds nothing); every query sees key 0, so at least one chunk is finite.
+// Merge of split items: one workgroup per (split item, wave slot, 32-dim block), eight
+// threads per query row of the slot, four dims (one float4 of a record) per thread, so a
+// launch spreads over 32 x as many workgroups as split items. Chunks combine by their
+// log2-sum-exp, eight at a time so their loads are in flight together (a chunk with
+// lse = -inf adds nothing; every query sees key 0, so at least one chunk is finite).
 // groups: per split item {request, q_begin, kv_head, head_group}, {first record, count}.
 template <int DT>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a, const int4* groups,
                                                             int waves_per_head, int hpb) {
   const int gi = blockIdx.x;
   const int slot = blockIdx.y;
+  const int db = blockIdx.z;
   const int4 w = groups[2 * gi];
   const int4 cnt = groups[2 * gi + 1];
   const ReqInfo rq = a.reqs[w.x];
   const int group = a.num_q_heads / a.num_kv_heads;
   const int qh = w.z * group + w.w * hpb + slot / waves_per_head;
   const int q = threadIdx.x >> 3;
-  const int part = threadIdx.x & 7;
+  const int g4 = (threadIdx.x >> 1) & 3;
+  const int h = threadIdx.x & 1;
   const int my_q = w.y + (slot % waves_per_head) * kQPerWave + q;
   if (my_q >= rq.q_len) return;
-  float mx = -INFINITY, den = 0.f, acc[16];
+  // Dims 32 db + 8 g4 + 4 h + i of query q sit in float4 (4 db + g4) * 64 + q + 32 h of a
+  // record (the main kernel's lane order).
+  const int f = (4 * db + g4) * 64 + q + 32 * h;
+  constexpr int kU = 8;
+  float mx = -INFINITY, den = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int c0 = 0; c0 < cnt.y; c0 += kU) {
+    float lse[kU];
+    float4 v[kU];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-  for (int c = 0; c < cnt.y; ++c) {
-    const int64_t rec = static_cast<int64_t>(cnt.x + c) * kWaves + slot;
-    const float lse = a.part_lse[rec * kQPerWave + q];
-    if (lse == -INFINITY) continue;
-    // Dims 16 part + 8 j + 4 h + i sit in float4 ((4 db + g4) * 64 + lane) of the record,
-    // db = part / 2, g4 = 2 (part % 2) + j, lane = q + 32 h (the main kernel's lane order).
-    const float* po = a.part_o + rec * (kQPerWave * kD);
-    float v[16];
+    for (int u = 0; u < kU; ++u) {
+      const int c = min(c0 + u, cnt.y - 1);
+      const int64_t rec = static_cast<int64_t>(cnt.x + c) * kWaves + slot;
+      lse[u] = c0 + u < cnt.y ? a.part_lse[rec * kQPerWave + q] : -INFINITY;
+      v[u] = *reinterpret_cast<const float4*>(a.part_o + rec * (kQPerWave * kD) + f * 4);
+    }
+    float m_new = mx;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int f = (4 * (part >> 1) + 2 * (part & 1) + j) * 64 + q + 32 * h;
-        const float4 x = *reinterpret_cast<const float4*>(po + f * 4);
-        v[8 * j + 4 * h] = x.x;
-        v[8 * j + 4 * h + 1] = x.y;
-        v[8 * j + 4 * h + 2] = x.z;
-        v[8 * j + 4 * h + 3] = x.w;
-      }
-    const float m_new = fmaxf(mx, lse);
+    for (int u = 0; u < kU; ++u) m_new = fmaxf(m_new, lse[u]);
+    if (m_new == -INFINITY) continue;  // no key of these chunks reaches this query yet
     const float corr = __builtin_amdgcn_exp2f(mx - m_new);
-    const float wgt = __builtin_amdgcn_exp2f(lse - m_new);
-    den = den * corr + wgt;
+    den *= corr;
+    acc = make_float4(acc.x * corr, acc.y * corr, acc.z * corr, acc.w * corr);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = fmaf(wgt, v[i], acc[i] * corr);
+    for (int u = 0; u < kU; ++u) {
+      const float wgt = __builtin_amdgcn_exp2f(lse[u] - m_new);  // 0 for lse = -inf
+      den += wgt;
+      acc = make_float4(fmaf(wgt, v[u].x, acc.x), fmaf(wgt, v[u].y, acc.y),
+                        fmaf(wgt, v[u].z, acc.z), fmaf(wgt, v[u].w, acc.w));
+    }
     mx = m_new;
   }
   const float inv = 1.f / den;
-  uint16_t* op = a.out + static_cast<int64_t>(rq.q_start + my_q) * a.o_sn + qh * a.o_sh +
-                 16 * part;
-  uint4 lo, hi;
-  lo.x = pack2<DT>(acc[0] * inv, acc[1] * inv);
-  lo.y = pack2<DT>(acc[2] * inv, acc[3] * inv);
-  lo.z = pack2<DT>(acc[4] * inv, acc[5] * inv);
-  lo.w = pack2<DT>(acc[6] * inv, acc[7] * inv);
-  hi.x = pack2<DT>(acc[8] * inv, acc[9] * inv);
-  hi.y = pack2<DT>(acc[10] * inv, acc[11] * inv);
-  hi.z = pack2<DT>(acc[12] * inv, acc[13] * inv);
-  hi.w = pack2<DT>(acc[14] * inv, acc[15] * inv);
-  *reinterpret_cast<uint4*>(op) = lo;
-  *reinterpret_cast<uint4*>(op + 8) = hi;
+  *reinterpret_cast<uint2*>(a.out + static_cast<int64_t>(rq.q_start + my_q) * a.o_sn +
+                            qh * a.o_sh + 32 * db + 8 * g4 + 4 * h) =
+      make_uint2(pack2<DT>(acc.x * inv, acc.y * inv), pack2<DT>(acc.z * inv, acc.w * inv));
 }
 
 __global__ __launch_bounds__(256) void pack_prefill_pages(const int32_t* __restrict__ table,
@@ -1003,8 +999,8 @@ void launch_dt(const PrefillArgs& a, int hpb, bool paged, const int4* groups,
   else if (hpb == 4) launch_prefill<DT, 4>(a, paged, s);
   else launch_prefill<DT, 8>(a, paged, s);
   if (num_groups)
-    prefill_merge_kernel<DT><<<dim3(static_cast<uint32_t>(num_groups), kWaves), dim3(256), 0,
-                               s>>>(a, groups, kWaves / hpb, hpb);
+    prefill_merge_kernel<DT><<<dim3(static_cast<uint32_t>(num_groups), kWaves, kD / 32),
+                               dim3(256), 0, s>>>(a, groups, kWaves / hpb, hpb);
 }
 }  // namespace
 }  // namespace mi355x
