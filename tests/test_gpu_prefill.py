@@ -248,16 +248,17 @@ def test_paged_small_prefixes_and_tiny_extends(gpu, seed):
             assert_close(out[bounds[r] + i], want[0], f"seed={seed} req={r} row={i}")
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_long_prefix_few_queries_is_split_along_keys(gpu, dtype):
+@pytest.mark.parametrize("dtype,page", [(torch.bfloat16, 16), (torch.float16, 16),
+                                        (torch.bfloat16, 3), (torch.bfloat16, 1)])
+def test_long_prefix_few_queries_is_split_along_keys(gpu, dtype, page):
     """A chunked-prefill continuation: one request with an 8,192-token cached prefix (random
-    page permutation) and 64 new tokens, beside a 3-token request, Hq32/Hkv8, page 16. That
+    page permutation) and 64 new tokens, beside a 3-token request, Hq32/Hkv8, pages of 16, 3
+    (the general copy path: pages that do not divide a 64-key tile) and 1. That
     is 16 work items for 256 CUs, so the plan cuts the long items along their keys and a
     merge launch combines the chunks (the reference's split-KV prefill plan,
     flashinfer_plan_run.cu:312-316); every row checked against the oracle."""
     rng = np.random.default_rng(21)
     g = torch.Generator().manual_seed(21)
-    page = 16
     pref = np.array([8192, 5])
     ext = np.array([64, 3])
     bounds = [0] + np.cumsum(ext).tolist()
@@ -283,17 +284,18 @@ def test_long_prefix_few_queries_is_split_along_keys(gpu, dtype):
         assert_close(out[bounds[r]:bounds[r + 1]], want[bounds[r]:bounds[r + 1]], f"req={r}")
 
 
-@pytest.mark.parametrize("hq,hkv", [(2, 2), (4, 2), (8, 1)])
-def test_single_long_sequence_is_split_along_keys(gpu, hq, hkv):
+@pytest.mark.parametrize("hq,hkv,dtype", [(2, 2, torch.bfloat16), (4, 2, torch.bfloat16),
+                                          (8, 1, torch.bfloat16), (4, 2, torch.float16)])
+def test_single_long_sequence_is_split_along_keys(gpu, hq, hkv, dtype):
     """One 2,000-token ragged sequence with few heads (query blocks of 256, 128 and 32
     queries): too few items for the device, so long items are split along their keys and
     merged; every row checked."""
     g = torch.Generator().manual_seed(hq * 10 + hkv)
     bounds = [0, 2000]
-    q = randn((2000, hq, 128), g, torch.bfloat16, gpu)
-    k = randn((2000, hkv, 128), g, torch.bfloat16, gpu)
-    v = randn((2000, hkv, 128), g, torch.bfloat16, gpu)
-    attn = make(gpu, hq, hkv, 16, torch.bfloat16)
+    q = randn((2000, hq, 128), g, dtype, gpu)
+    k = randn((2000, hkv, 128), g, dtype, gpu)
+    v = randn((2000, hkv, 128), g, dtype, gpu)
+    attn = make(gpu, hq, hkv, 16, dtype)
     table = torch.zeros(1, 128, dtype=torch.int32, device=gpu)
     batch = attn.prepare(meta_for(gpu, bounds, [0], table), 2000)
     assert batch.plan.plan.info()["split_items"] > 0
