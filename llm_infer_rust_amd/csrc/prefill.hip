@@ -338,8 +338,6 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
   const int my_q = wq0 + col;
   const int my_horizon = rq.prefix + my_q;
 
-  // One 64-key tile per step: S^T = K Q^T (two 32-key blocks), mask and row max, lazy
-  // rescale, P^T = 2^(s scale - m), O^T += V^T P^T.
   // One 64-key tile per step: S^T = K Q^T - m (two 32-key blocks), mask and row max,
   // lazy rescale, P^T = 2^(S^T), O^T += V^T P^T.
   auto compute = [&](int t, int stage, bool first) {
@@ -470,8 +468,9 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
   }
   // The wave's 32 x 128 output tile goes out as whole 256-byte rows: written to an LDS
   // region no wave reads any more (a stage other than the last tile's; waves 0-3 and 4-7
-  // take two different stages, 8 KB each, 16-byte chunks XOR-swizzled by row so both the
-  // column writes and the row reads are conflict-free), then read back row-major.
+  // take two different stages, 8 KB each, 16-byte chunks XOR-swizzled by row so the row
+  // reads are conflict-free and the column writes nearly so: rows r and r + 16 share
+  // banks), then read back row-major.
   // (Lane-order stores of 16 bytes per query row cost ~4.8 us per item at config 3.)
   const float inv = 1.f / row_sum;
   uint8_t* tile = lds + ((nt + (wave >> 2)) % STAGES) * kStageBytes + (wave & 3) * 8192;
