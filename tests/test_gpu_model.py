@@ -11,6 +11,7 @@ import pytest
 import torch
 
 from engine_helpers import RecordingEngine
+from llm_infer_rust_amd.backend import BatchPhase
 from llm_infer_rust_amd.batch import BatchRequest
 from llm_infer_rust_amd.engine import Engine, EngineConfig
 from llm_infer_rust_amd.model import Qwen3Config, Qwen3Model
@@ -175,3 +176,33 @@ def test_config1_shape_greedy_tokens_match_oracle(gpu):
           f"gap {min(gaps):.4f}")
     if same < 64:
         assert gaps[same] <= 2 * errs[same], (same, gaps[same], errs[same])
+
+
+def test_chunked_long_prompt_uses_split_prefill(gpu):
+    """A 2,100-token prompt through a 512-token prefill budget: the later chunks are paged
+    prefills over long cached prefixes with few items for the device, which the plan splits
+    along the keys (split-KV + merge). The first generated tokens must stay within the bf16
+    error bound of the oracle's argmax, teacher-forced."""
+    model, oracle = build(TINY, 7, gpu)
+    eng = Engine(model, EngineConfig(page_size=16, max_running_req=2,
+                                     max_prefill_tokens_per_batch=512, max_seq_len=2200,
+                                     use_graphs=False))
+    prompt = np.random.default_rng(8).integers(0, TINY.vocab_size, 2100)
+    seen = []
+    real_prepare = model.attention.prepare
+
+    def spy(meta, n):
+        batch = real_prepare(meta, n)
+        if meta.forward_mode == BatchPhase.PREFILL:
+            seen.append(batch.plan.plan.info()["split_items"])
+        return batch
+
+    model.attention.prepare = spy
+    try:
+        req = eng.add_request(prompt, SamplingParams(max_tokens=4))
+        eng.run_until_complete()
+    finally:
+        model.attention.prepare = real_prepare
+    assert eng.stats["prefill_batches"] == 5 and max(seen) > 0, seen
+    assert len(req.output) == 4
+    check_teacher_forced(oracle, prompt, req.output, tol=0.05)
