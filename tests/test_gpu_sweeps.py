@@ -126,3 +126,41 @@ def test_prefill_sweep(gpu, case):
     assert_close(f32(out).reshape(want.shape), want,
                  f"case {case}: hq={hq} hkv={hkv} paged={paged} page={page} ext={ext.tolist()} "
                  f"prefixes={prefixes.tolist()} {dtype}")
+
+
+@pytest.mark.parametrize("page", [64, 128])
+def test_large_pages_decode_and_paged_prefill(gpu, page):
+    """Pages of a whole prefill key tile (64) and larger (128, the general copy path), for
+    decode and for paged prefill over cached prefixes (ending mid-page and on page borders)."""
+    rng = np.random.default_rng(page)
+    g = torch.Generator().manual_seed(page)
+    hq, hkv, dtype = 32, 8, torch.bfloat16
+    lengths = np.array([1, 63, 64, 65, 129, 700, 2 * page, 2000], np.int32)
+    table, pool = page_table(rng, lengths, page)
+    kc = torch.randn(pool, page, hkv, 128, generator=g).to(dtype).to(gpu)
+    vc = torch.randn(pool, page, hkv, 128, generator=g).to(dtype).to(gpu)
+    cache = BaseAttention()
+    cache.bind_kv_cache(kc, vc)
+    attn = backend(gpu, hq, hkv, page, dtype)
+    b = lengths.size
+    q = torch.randn(b, hq, 128, generator=g).to(dtype).to(gpu)
+    meta = AttentionMetadata(BatchPhase.DECODE, block_table=torch.from_numpy(table).to(gpu),
+                             cache_seqlens=torch.from_numpy(lengths).to(gpu))
+    out = attn.prepare(meta, b).forward(q, q, q, cache)
+    want = oatt.decode_with_cache(f32(q), f32(kc), f32(vc), table, lengths, page)
+    assert_close(f32(out).reshape(want.shape), want, f"decode page={page}")
+    # Paged prefill: the last `ext` tokens of each request are the new queries.
+    ext = np.minimum(lengths, np.array([1, 5, 64, 1, 70, 33, 3, 130]))
+    pref = lengths - ext
+    bounds = [0] + np.cumsum(ext).tolist()
+    n = bounds[-1]
+    qp = torch.randn(n, hq, 128, generator=g).to(dtype).to(gpu)
+    meta = AttentionMetadata(BatchPhase.PREFILL,
+                             cu_seqlens_q=torch.tensor(bounds, dtype=torch.int32, device=gpu),
+                             prefix_lens=torch.tensor(pref.tolist(), dtype=torch.int32, device=gpu),
+                             block_table=torch.from_numpy(table).to(gpu))
+    batch = attn.prepare(meta, n)
+    assert batch.plan.plan.paged
+    got = f32(batch.forward(qp, qp, qp, cache)).reshape(n, hq, 128)
+    want = oatt.prefill_with_cache(f32(qp), f32(kc), f32(vc), table, bounds, pref, page)
+    assert_close(got, want, f"prefill page={page}")
