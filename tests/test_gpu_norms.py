@@ -155,3 +155,21 @@ def test_config3_norm_shapes(gpu):
     check(q, want_q, torch.bfloat16, 0.03125)
     check(k, want_k, torch.bfloat16, 0.03125)
     assert torch.equal(packed[:, 3072:], vb)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_qk_norm_many_rows_with_a_ragged_tail(gpu, dtype):
+    """1,367 tokens x (16 + 8) heads = 32,808 head rows: the multi-row narrow kernel, with a
+    last workgroup that is only partly filled (32,808 is not a multiple of its 32 rows)."""
+    g = torch.Generator().manual_seed(47)
+    packed = torch.randn(1367, 4096, generator=g).to(dtype).to(gpu)
+    q = packed[:, :2048].view(-1, 16, 128)
+    k = packed[:, 2048:3072].view(-1, 8, 128)
+    qw = torch.empty(128).uniform_(0.5, 1.5, generator=g).to(dtype).to(gpu)
+    kw = torch.empty(128).uniform_(0.5, 1.5, generator=g).to(dtype).to(gpu)
+    want_q, want_k = onorm.qk_norm_f32(f32(q), f32(k), f32(qw), f32(kw), 1e-6)
+    vb = packed[:, 3072:].clone()
+    ops.qk_norm(q, k, qw, kw, 1e-6)
+    check(q, want_q, dtype, TOL[dtype][0])
+    check(k, want_k, dtype, TOL[dtype][0])
+    assert torch.equal(packed[:, 3072:], vb)
