@@ -185,6 +185,83 @@ __global__ __launch_bounds__(256) void norm_vec16_rows(NormArgs a) {
   }
 }
 
+// Many rows, RPT rows per LPR-lane group: a group's rows sit (256 / LPR) groups apart and
+// all RPT rows' loads (data and weights) are issued before the first reduction, so each
+// lane keeps RPT times as many 16-byte loads in flight as one row allows. Rows past the end
+// are masked per group (the group's lanes share a row, so the reductions stay in it).
+template <int DT, int MODE, int LPR, int NCH, int RPT>
+__global__ __launch_bounds__(256) void norm_vec_rows(NormArgs a) {
+  constexpr int kGroups = 256 / LPR;
+  const int lane = threadIdx.x % LPR;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kGroups * RPT + threadIdx.x / LPR;
+  const int chunks = static_cast<int>(a.width >> 3);
+  uint16_t* dst[RPT];
+  uint16_t* res[RPT];
+  uint4 raw[RPT][NCH], wraw[RPT][NCH], rraw[RPT][NCH];
+  bool ok[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int64_t row = row0 + kGroups * k;
+    ok[k] = row < a.rows;
+    uint16_t* src;
+    const uint16_t* w;
+    row_pointers<MODE>(a, ok[k] ? row : 0, src, dst[k], res[k], w);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int chunk = lane + c * LPR;
+      if (ok[k] && chunk < chunks) {
+        wraw[k][c] = ld128(w + chunk * 8);
+        raw[k][c] = ld128(src + chunk * 8);
+        if constexpr (MODE == kAddRms) rraw[k][c] = ld128(res[k] + chunk * 8);
+      }
+    }
+  }
+  float ss[RPT];
+  float vals[RPT][NCH][8];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    ss[k] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int chunk = lane + c * LPR;
+      if (ok[k] && chunk < chunks) {
+        unpack8<DT>(raw[k][c], vals[k][c]);
+        if constexpr (MODE == kAddRms) {
+          float r[8];
+          unpack8<DT>(rraw[k][c], r);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) vals[k][c][i] += r[i];
+          st128(res[k] + chunk * 8, pack8<DT>(vals[k][c]));
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss[k] = fmaf(vals[k][c][i], vals[k][c][i], ss[k]);
+      }
+    }
+  }
+  if constexpr (LPR == 16) {
+    row16_sum_n<RPT>(ss);
+  } else {
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) ss[k] = wave_sum(ss[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const float scale = rsqrtf(ss[k] / static_cast<float>(a.width) + a.eps);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int chunk = lane + c * LPR;
+      if (ok[k] && chunk < chunks) {
+        float wf[8];
+        unpack8<DT>(wraw[k][c], wf);
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = (vals[k][c][i] * scale) * wf[i];
+        st128(dst[k] + chunk * 8, pack8<DT>(y));
+      }
+    }
+  }
+}
+
 // Few wide rows (decode-size batches of hidden rows): one 256-lane workgroup per
 // row so a batch of a few hundred rows still spreads over every CU. Each lane
 // holds NCH 128-bit chunks; the sum of squares crosses waves through LDS.
@@ -279,6 +356,13 @@ const char* dispatch(const NormArgs& a, bool vec, hipStream_t s, const char* nam
     // <= 128 elements, many rows: 16 lanes per row, kNarrowRows rows per lane group.
     const int64_t blocks = (a.rows + 16 * kNarrowRows - 1) / (16 * kNarrowRows);
     norm_vec16_rows<DT, MODE, kNarrowRows>
+        <<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, s>>>(a);
+    return launch_status(name);
+  }
+  if (vec && MODE == kRms && chunks > 64 && chunks <= 128) {
+    // 513..1024 elements, no residual: one wave per row, both chunks' loads up front.
+    const int64_t blocks = (a.rows + 3) / 4;
+    norm_vec_rows<DT, MODE, 64, 2, 1>
         <<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, s>>>(a);
     return launch_status(name);
   }
