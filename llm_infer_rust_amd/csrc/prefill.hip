@@ -201,8 +201,9 @@ __global__ __launch_bounds__(64 * kWaves, 1) void prefill_kernel(PrefillArgs a) 
     // loop's scores come out of the matrix cores already in the exp2 domain.
 #pragma unroll
     for (int s = 0; s < 8; ++s) qreg[s] = scale_row8<DT>(qreg[s], a.scale_log2);
-    // Pin the scaled rows in registers: without this the compiler, short of registers,
-    // keeps the raw rows instead and redoes the scaling (about 180 VALU) in every tile.
+    // Keep the scaled rows in registers behind an empty asm the compiler cannot look
+    // through, so the scaling can never be rematerialised inside the tile loop (at 250+
+    // VGPRs that would be the cheap way out for the register allocator).
 #pragma unroll
     for (int s = 0; s < 8; ++s)
       asm volatile("" : "+v"(qreg[s].x), "+v"(qreg[s].y), "+v"(qreg[s].z), "+v"(qreg[s].w));
