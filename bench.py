@@ -524,6 +524,24 @@ def ceilings_section(dev, w, reps: int) -> dict:
         blocks, iters, ctypes.c_void_p(sink.data_ptr()), stream)), 5)
     flops = blocks * 8 * iters * 32 * 32768
     out["attention_core_random"] = {"TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}
+    # The same work as 8 waves x 32 queries and as 4 waves x 64 queries (half the LDS
+    # reads), each workgroup's shader cycles read back: cycles per tile, and the clock the
+    # chip held (one workgroup per CU at a time, blocks / CUs of them per CU in sequence).
+    lib.mi355x_calib_attention_core_cycles.restype = ctypes.c_char_p
+    cycles = torch.zeros(blocks, dtype=torch.int64, device=dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    per_cu = blocks / cus
+    core = {}
+    for variant, name in ((0, "waves8_q32"), (1, "waves4_q64")):
+        ms = timed(lambda i, v=variant: check(lib.mi355x_calib_attention_core_cycles(
+            blocks, iters, v, ctypes.c_void_p(cycles.data_ptr()), ctypes.c_void_p(sink.data_ptr()),
+            stream)), 5)
+        mean = float(cycles.double().mean())
+        core[name] = {"TFLOP/s": round(blocks * iters * 2 ** 23 / (ms * 1e-3) / 1e12, 1),
+                      "cycles_per_tile": round(mean / iters),
+                      "GHz": round(mean * per_cu / (ms * 1e6), 3),
+                      "ns_per_tile": round(ms * 1e6 / (per_cu * iters), 1)}
+    out["attention_core_cycles"] = core
     return out
 
 

@@ -12,7 +12,12 @@
 //           clock under this load, so the rate is below the nominal dense peak;
 //   core:   the prefill kernel's per-tile work on LDS-resident random tiles, 8 waves per
 //           workgroup: S^T = K Q^T (16 MFMAs), row max, exp2, P^T packing and row sums,
-//           O^T += V^T P^T (16 MFMAs with transposed LDS reads), one barrier per tile.
+//           O^T += V^T P^T (16 MFMAs with transposed LDS reads), one barrier per tile;
+//   core64: the same work as 4 waves of 64 queries (one wave per SIMD, each K and V
+//           fragment feeding two products, half the LDS reads). Both report the shader
+//           cycles of every workgroup, so a run gives cycles per tile and the clock the
+//           chip held: the two structures take different cycle counts per tile at
+//           different clocks for nearly the same time, the signature of a power limit.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -121,7 +126,9 @@ __global__ __launch_bounds__(512) void mfma_random(float* sink, int iters) {
 
 constexpr int kStage = 32768;  // one 64-key K tile + one V tile, bf16, head_dim 128
 
-__global__ __launch_bounds__(512, 1) void attention_core(float* sink, int iters) {
+__global__ __launch_bounds__(512, 1) void attention_core(float* sink, int iters,
+                                                         uint64_t* cycles) {
+  const uint64_t c_start = __builtin_readcyclecounter();
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStage];
   const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, half = lane >> 5;
   for (int i = tid; i < 2 * kStage / 4; i += 512)
@@ -217,6 +224,128 @@ __global__ __launch_bounds__(512, 1) void attention_core(float* sink, int iters)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc += o[db][r];
   if (acc == 1234.5f) sink[0] = acc;
+  if (cycles && threadIdx.x == 0) cycles[blockIdx.x] = __builtin_readcyclecounter() - c_start;
+}
+
+// The same per-tile work as 4 waves of 64 queries: per wave two 32-query blocks, so each K
+// fragment (S^T) and each V^T fragment (O^T) feeds two products.
+__global__ __launch_bounds__(256, 1) void attention_core64(float* sink, int iters,
+                                                           uint64_t* cycles) {
+  const uint64_t c_start = __builtin_readcyclecounter();
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * kStage];
+  const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, half = lane >> 5;
+  for (int i = tid; i < 2 * kStage / 4; i += 256)
+    reinterpret_cast<uint32_t*>(lds)[i] = random_bf16x2(mix(i + blockIdx.x * 977u));
+  __syncthreads();
+  uint4 q[2][8];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int s = 0; s < 8; ++s) q[b][s] = random_operand((blockIdx.x * 512 + 2 * tid + b) * 64 + s * 4);
+  const int gq = lane >> 4, p16 = lane & 15;
+  const int v_key = 4 * (gq >> 1) + (p16 >> 2);
+  const int v_lo = 2 * (gq & 1) + ((p16 >> 1) & 1);
+  int v_off[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+    v_off[db] = 16384 + v_key * 256 + ((4 * db + v_lo) ^ (4 * (p16 >> 2))) * 16 + 8 * (p16 & 1);
+  floatx16 o[4][2];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][b][r] = 0.f;
+  float m[2] = {0.f, 0.f}, l[2] = {0.f, 0.f};
+  for (int t = 0; t < iters; ++t) {
+    __syncthreads();
+    const uint8_t* sb = lds + (t & 1) * kStage;
+    floatx16 s[2][2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[0][b][r] = s[1][b][r] = -m[b];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+      for (int T = 0; T < 2; ++T) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(
+            sb + (32 * T + col) * 256 + (((2 * kk + half) ^ (col & 15)) * 16));
+#pragma unroll
+        for (int b = 0; b < 2; ++b) s[T][b] = mfma(kf, q[b][kk], s[T][b]);
+      }
+    float mx[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      float v = -INFINITY;
+#pragma unroll
+      for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v = fmaxf(v, s[T][b][r]);
+      const auto sw =
+          __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+      mx[b] = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    if (__any(mx[0] > 8.f || mx[1] > 8.f)) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const float shift = fmaxf(mx[b], 0.f);
+        const float alpha = __builtin_amdgcn_exp2f(-shift);
+        m[b] += shift;
+        l[b] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[db][b][r] *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          s[0][b][r] -= shift;
+          s[1][b][r] -= shift;
+        }
+      }
+    }
+    uint4 pb[4][2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      float ls[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int T = 0; T < 2; ++T)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          float p[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            p[i] = __builtin_amdgcn_exp2f(s[T][b][8 * hh + i]);
+            ls[i & 3] += p[i];
+          }
+          pb[2 * T + hh][b] = make_uint4(pack2(p[0], p[1]), pack2(p[2], p[3]),
+                                         pack2(p[4], p[5]), pack2(p[6], p[7]));
+        }
+      l[b] += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        lds_u8* vp = (lds_u8*)sb + v_off[db] + 16 * kk * 256;
+        const uint2 lo =
+            __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)vp));
+        const uint2 hi = __builtin_bit_cast(
+            uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vp + 8 * 256)));
+        const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) o[db][b] = mfma(vf, pb[kk][b], o[db][b]);
+      }
+  }
+  float acc = l[0] + l[1];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc += o[db][b][r];
+  if (acc == 1234.5f) sink[0] = acc;
+  if (cycles && threadIdx.x == 0) cycles[blockIdx.x] = __builtin_readcyclecounter() - c_start;
 }
 
 }  // namespace
@@ -268,6 +397,23 @@ extern "C" __attribute__((visibility("default"))) const char* mi355x_calib_mfma(
 extern "C" __attribute__((visibility("default"))) const char* mi355x_calib_attention_core(
     int32_t blocks, int32_t iters, void* sink, void* stream) {
   attention_core<<<blocks, 512, 0, static_cast<hipStream_t>(stream)>>>(static_cast<float*>(sink),
-                                                                       iters);
+                                                                       iters, nullptr);
+  return hipGetLastError() == hipSuccess ? nullptr : "attention core launch failed";
+}
+
+// One launch of the per-tile work with each workgroup's shader cycles written to
+// `cycles` (blocks x uint64): variant 0 is the 8-wave x 32-query structure of
+// mi355x_calib_attention_core, variant 1 the 4-wave x 64-query one. Both cover 256 query
+// rows x 64 keys x 128 dims per workgroup and tile: FLOPs = blocks * iters * 2^23.
+extern "C" __attribute__((visibility("default"))) const char* mi355x_calib_attention_core_cycles(
+    int32_t blocks, int32_t iters, int32_t variant, void* cycles, void* sink, void* stream) {
+  auto s = static_cast<hipStream_t>(stream);
+  auto c = static_cast<uint64_t*>(cycles);
+  if (variant == 0)
+    attention_core<<<blocks, 512, 0, s>>>(static_cast<float*>(sink), iters, c);
+  else if (variant == 1)
+    attention_core64<<<blocks, 256, 0, s>>>(static_cast<float*>(sink), iters, c);
+  else
+    return "attention core variant must be 0 or 1";
   return hipGetLastError() == hipSuccess ? nullptr : "attention core launch failed";
 }
