@@ -94,15 +94,17 @@ def test_linear_workspace_bytes_query(native):
     assert f(256, 4096, 12288, 256, -1, -1) > 0
 
 
+@pytest.mark.parametrize("ragged", [False, True])
 @pytest.mark.parametrize("seed", range(5))
-def test_prefill_schedule_covers_every_query_block_once(native, seed):
-    """mi355x_prefill_schedule: every (request, 32 x 8 / heads-per-block query block, kv
-    head, head group) appears exactly once, and items come longest causal horizon first."""
+def test_prefill_schedule_covers_every_query_block_once(native, seed, ragged):
+    """mi355x_prefill_schedule: every (request, 32 x waves / heads-per-block query block, kv
+    head, head group) appears exactly once, and items come longest causal horizon first.
+    Batches with a cached prefix run 8-wave workgroups, batches without one 4-wave ones."""
     rng = np.random.default_rng(seed)
     b = int(rng.integers(1, 12))
     hq, hkv = [(16, 8), (32, 8), (8, 8), (64, 8), (8, 1)][seed]
     q_lens = rng.integers(1, 900, size=b)
-    prefixes = rng.integers(0, 3000, size=b) * (rng.random(b) < 0.5)
+    prefixes = rng.integers(0, 3000, size=b) * (rng.random(b) < 0.5) * (not ragged)
     q_host = (ctypes.c_int32 * (b + 1))(*([0] + np.cumsum(q_lens).tolist()))
     p_host = (ctypes.c_int32 * b)(*prefixes.tolist())
     lib = native.lib()
@@ -111,8 +113,9 @@ def test_prefill_schedule_covers_every_query_block_once(native, seed):
     assert lib.mi355x_prefill_schedule(q_host, p_host, b, hq, hkv, work, n) == n
     items = np.array(list(work), dtype=np.int64).reshape(n, 4)
     group = hq // hkv
-    hpb = min(group, 8)
-    bq = 32 * (8 // hpb)
+    waves = 8 if (prefixes > 0).any() else 4
+    hpb = min(group, waves)
+    bq = 32 * (waves // hpb)
     want = {(r, q0, h, g) for r in range(b) for q0 in range(0, int(q_lens[r]), bq)
             for h in range(hkv) for g in range(group // hpb)}
     got = [tuple(int(v) for v in row) for row in items]
