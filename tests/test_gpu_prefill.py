@@ -287,7 +287,7 @@ def test_long_prefix_few_queries_is_split_along_keys(gpu, dtype, page):
 @pytest.mark.parametrize("hq,hkv,dtype", [(2, 2, torch.bfloat16), (4, 2, torch.bfloat16),
                                           (8, 1, torch.bfloat16), (4, 2, torch.float16)])
 def test_single_long_sequence_is_split_along_keys(gpu, hq, hkv, dtype):
-    """One 2,000-token ragged sequence with few heads (query blocks of 256, 128 and 32
+    """One 2,000-token ragged sequence with few heads (4-wave items of 128, 64 and 32
     queries): too few items for the device, so long items are split along their keys and
     merged; every row checked."""
     g = torch.Generator().manual_seed(hq * 10 + hkv)
