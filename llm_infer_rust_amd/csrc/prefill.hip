@@ -607,8 +607,8 @@ struct Buffer {
 // ranges per item, and 8-wave workgroups (one per CU, 256 query rows per item) read each
 // K/V tile for twice the rows; a batch without one (ragged, every item a causal triangle
 // or part of one) runs 4-wave workgroups, two per CU, so one workgroup's prologue, epilogue
-// and barriers overlap the other's tiles (measured on config 3 and on the 8 x 1024-token
-// Qwen3-8B prompt batch: 4% faster; on config 4's long prefixes 8 waves are 5% faster).
+// and barriers overlap the other's tiles (measured: config 3 1.5% faster, the 8 x 1024-token
+// Qwen3-8B prompt batch 6% faster; on config 4's long prefixes 8 waves are 5% faster).
 // MI355X_PREFILL_WAVES=8 keeps 8 waves for every batch (tuning knob, read once).
 int prefill_waves(bool paged) {
   static const bool force8 = [] {
