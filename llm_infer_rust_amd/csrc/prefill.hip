@@ -172,10 +172,11 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void prefill_kernel(Prefi
   const int q_begin = w.y;
   const int kvh = w.z;
   const int group = a.num_q_heads / a.num_kv_heads;
-  // Waves w and w + 4 share a SIMD. The upper four waves take their (head, query slot)
-  // in mirrored order, so each SIMD pairs an early query slot with a late one and the
-  // causal tiles near the diagonal, where late slots still work and early ones are
-  // done, are spread over all four SIMDs.
+  // In an 8-wave workgroup waves w and w + 4 share a SIMD. The upper four waves take
+  // their (head, query slot) in mirrored order, so each SIMD pairs an early query slot
+  // with a late one and the causal tiles near the diagonal, where late slots still work
+  // and early ones are done, are spread over all four SIMDs. (A 4-wave workgroup has one
+  // wave per SIMD; its partner is a wave of the CU's other workgroup.)
   static_assert(NW == 8 || NW == 4, "8 or 4 waves per workgroup");
   const int slot_id = NW == 8 && wave >= 4 ? 11 - wave : wave;
   const int qh = kvh * group + w.w * HPB + slot_id / kWavesPerHead;
@@ -475,8 +476,9 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void prefill_kernel(Prefi
     return;
   }
   // The wave's 32 x 128 output tile goes out as whole 256-byte rows: written to an LDS
-  // region no wave reads any more (a stage other than the last tile's; waves 0-3 and 4-7
-  // take two different stages, 8 KB each, 16-byte chunks XOR-swizzled by row so the row
+  // region no wave reads any more (a stage other than the last tile's: every wave has
+  // passed the barrier after finishing the tiles before it; waves 0-3 and 4-7 take two
+  // different stages, 8 KB each, 16-byte chunks XOR-swizzled by row so the row
   // reads are conflict-free and the column writes nearly so: rows r and r + 16 share
   // banks), then read back row-major.
   // (Lane-order stores of 16 bytes per query row cost ~4.8 us per item at config 3.)
