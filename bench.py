@@ -107,7 +107,58 @@ def e2e_section(dev, args) -> dict:
     }
     del eng, model
     torch.cuda.empty_cache()
+    if not getattr(args, "no_cpu_baseline", False):
+        result["cpu_baseline"] = e2e_cpu_baseline(args.seed)
     return result
+
+
+def e2e_cpu_baseline(seed: int) -> dict:
+    """Host-CPU reference for config 5 (reported baseline): the oracle's numpy fp32
+    restatement of the reference CPU eager forward (model.rs:155-534, `pt` backend) at the
+    Qwen3-8B widths, one request: a 1024-token prefill (logits of the last row only, as the
+    reference computes them at logits_indices) and 8 cached decode steps, timed with 1 and
+    with 2 decoder layers. Each time is a fixed part (embedding, final norm, lm_head) plus a
+    per-layer part; the two fits give the 36-layer model's TTFT and per-token decode time."""
+    import dataclasses
+    import numpy as np
+    from llm_infer_rust_amd.model import Qwen3Config
+    from oracle import qwen3 as oq  # the CPU baseline only
+
+    cfg8 = Qwen3Config.qwen3_8b()
+    cfg2 = dataclasses.replace(cfg8, num_layers=2, max_position_embeddings=2048)
+    cfg1 = dataclasses.replace(cfg2, num_layers=1)
+    w2 = oq.random_weights(cfg2, seed)
+    w1 = {k: v for k, v in w2.items() if not k.startswith("model.layers.1.")}
+    prompt = np.random.default_rng(seed).integers(0, cfg8.vocab_size, 1024)
+    steps = 8
+    times = {}
+    for layers, cfg, w in ((1, cfg1, w1), (2, cfg2, w2)):
+        m = oq.Qwen3Oracle(cfg, w)
+        t0 = time.perf_counter()
+        tok = int(np.argmax(m.forward(prompt, 0, last_only=True)[-1]))
+        t_pre = time.perf_counter() - t0
+        pos = prompt.size
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            tok = int(np.argmax(m.forward(np.array([tok]), pos)[-1]))
+            pos += 1
+        times[layers] = (t_pre, (time.perf_counter() - t0) / steps)
+        del m
+    del w1, w2
+
+    def at_36(i):
+        per_layer = times[2][i] - times[1][i]
+        return times[1][i] - per_layer + cfg8.num_layers * per_layer
+
+    ttft_s, token_s = at_36(0), at_36(1)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    return {"value": round(1.0 / token_s, 3), "unit": "output tok/s (one request)",
+            "ttft_ms": round(ttft_s * 1e3, 1), "cores": threads, "kind": "port",
+            "sample": ("numpy fp32 restatement of the reference CPU eager forward at the "
+                       "Qwen3-8B widths, one request: 1024-token prefill + 8 decode steps "
+                       "timed at 1 and 2 layers, fixed + per-layer parts extrapolated to 36 "
+                       f"layers (measured: prefill {times[1][0]:.2f} / {times[2][0]:.2f} s, "
+                       f"decode {times[1][1] * 1e3:.0f} / {times[2][1] * 1e3:.0f} ms per token)")}
 
 
 METRIC = "decode-attn HBM GB/s (% peak); prefill MFMA util; output tok/s Qwen3-8B"

@@ -47,8 +47,9 @@ class Qwen3Oracle:
         return attention.attention_against_cache(q, k_all, v_all, start, cfg.num_attention_heads,
                                                  cfg.num_kv_heads).astype(np.float32)
 
-    def forward(self, ids: np.ndarray, start: int) -> np.ndarray:
-        """Append ``ids`` at positions start.. to the cache; return logits for every row."""
+    def forward(self, ids: np.ndarray, start: int, last_only: bool = False) -> np.ndarray:
+        """Append ``ids`` at positions start.. to the cache; return logits for every row (or
+        only the last, as the reference computes them only at ``logits_indices``)."""
         cfg, w = self.cfg, self.w
         ids = np.asarray(ids, np.int64)
         t = ids.size
@@ -81,6 +82,8 @@ class Qwen3Oracle:
             x, r = norms.add_rms_norm_f32(o, r, w[p + "post_attention_layernorm.weight"], eps)
             gu = x @ w[p + "mlp.gate_up_proj.weight"].T
             h = layer_ops.silu_mul(gu) @ w[p + "mlp.down_proj.weight"].T
+        if last_only:
+            h, r = h[-1:], r[-1:]
         h, _ = norms.add_rms_norm_f32(h, r, w["model.norm.weight"], eps)
         lm = w["model.embed_tokens.weight"] if cfg.tie_word_embeddings else w["lm_head.weight"]
         return (h @ lm.T).astype(np.float32)

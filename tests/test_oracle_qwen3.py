@@ -27,6 +27,16 @@ def test_cached_and_chunked_forward_match_full_forward():
     np.testing.assert_allclose(np.concatenate(parts), full, atol=1e-4, rtol=1e-4)
 
 
+def test_last_only_logits_are_the_last_row():
+    w = oq.random_weights(TINY, 6, std=0.05)
+    ids = np.random.default_rng(7).integers(0, TINY.vocab_size, 17)
+    full = oq.Qwen3Oracle(TINY, w).forward(ids, 0)
+    last = oq.Qwen3Oracle(TINY, w).forward(ids, 0, last_only=True)
+    assert last.shape == (1, TINY.vocab_size)
+    # (a one-row product and a 17-row one round differently inside BLAS)
+    np.testing.assert_allclose(last[0], full[-1], rtol=1e-5, atol=1e-5)
+
+
 def test_tied_embeddings_use_the_embedding_matrix():
     cfg = Qwen3Config(**{**TINY.__dict__, "tie_word_embeddings": True})
     w = oq.random_weights(cfg, 5)
