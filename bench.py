@@ -175,7 +175,7 @@ def parse_args():
                    help="requests in the bounded CPU-baseline sample")
     p.add_argument("--decode-only", action="store_true",
                    help="skip the prefill and norm measurements")
-    p.add_argument("--only", choices=["prefill", "norms", "e2e", "ceilings"],
+    p.add_argument("--only", choices=["prefill", "norms", "e2e", "ceilings", "serving_ops"],
                    help="print only this section's measurements (tuning aid)")
     p.add_argument("--e2e-requests", type=int, default=256)
     p.add_argument("--e2e-input", type=int, default=1024)
@@ -596,6 +596,163 @@ def ceilings_section(dev, w, reps: int) -> dict:
     return out
 
 
+def _cpu_single_ms(fn, runs: int = 3) -> float:
+    """Median wall time of a single-threaded (numpy) host routine after one warm-up run."""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return sorted(times)[len(times) // 2]
+
+
+def serving_ops_section(dev, reps: int, cpu: bool = True) -> dict:
+    """The config-5 kernels around the attention path at its shapes, each timed over `reps`
+    launches with HIP events, with the bytes (or FLOPs) it moves and a reported CPU baseline:
+    joint top-k / top-p sampling of 256 rows x 151,936 (sampling.rs:239-321),
+    the fused QK-norm -> RoPE -> K/V store pass of a 256-row decode step and of an 8192-token
+    prompt batch, SiLU x mul of the prompt batch, and the four decode-batch projections at 256
+    rows (row f3; fused_ops.cu:108-171,340-372, linear.rs). The projections rotate over two
+    weight sets (~770 MB) so the weights stream from HBM, as in serving."""
+    import numpy as np
+    from llm_infer_rust_amd import ops
+    from llm_infer_rust_amd.kv_cache import BaseAttention
+    from llm_infer_rust_amd.sampling import Sampler, SamplingParams
+
+    gd = torch.Generator(device=dev).manual_seed(9)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=gd, device=dev) * scale).to(torch.bfloat16)
+
+    out = {}
+    # Sampling (T 0.7, top-k 50, top-p 0.9, as config 5).
+    rows, vocab = 256, 151936
+    logits = rnd(rows, vocab, scale=2.0)
+    sampler = Sampler(2)
+    params = [SamplingParams(temperature=0.7, top_k=50, top_p=0.9)] * rows
+    ids = torch.empty(rows, dtype=torch.int64, device=dev)
+    ms = _event_time_ms(lambda: sampler.sample_batch_device(logits, params, out=ids), reps)
+    nbytes = rows * vocab * 2
+    res = {"us": round(ms * 1e3, 2), "rows/s": round(rows / (ms * 1e-3), 1), "bytes": nbytes,
+           "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+           "note": "one pass over the logits; the kernel makes up to five (the row stays in L2)"}
+    if cpu:
+        from oracle import sampling as osamp  # the CPU baseline only
+        sample = logits[:8].float().cpu().numpy()
+        t8, k8, p8 = np.full(8, 0.7, np.float32), np.full(8, 50), np.full(8, 0.9, np.float32)
+        cms = _cpu_single_ms(lambda: osamp.sample_rows(sample, t8, k8, p8, 2, 0))
+        res["cpu_baseline"] = {
+            "value": round(8 / (cms * 1e-3), 2), "unit": "rows/s", "cores": 1, "kind": "port",
+            "sample": "8 of the 256 rows, numpy restatement of the joint top-k/top-p rule with "
+                      "the same Philox/Gumbel draw, median of 3"}
+    out["sample_256x151936"] = res
+    del logits
+
+    # Fused QK-norm -> RoPE -> K/V store (Qwen3-8B heads: 32 q, 8 kv, head_dim 128).
+    rope = ops.HalfSplitRope(40960, 128, 1_000_000.0, dev)
+    pages = 8192
+    kc = torch.zeros(pages, 16, 8, 128, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    att = BaseAttention()
+    att.set_reserved_write_slot(0)
+    att.bind_kv_cache(kc, vc)
+    qw = (torch.rand(128, generator=gd, device=dev) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(128, generator=gd, device=dev) + 0.5).to(torch.bfloat16)
+    for name, t in (("head_rows_decode_256", 256), ("head_rows_prefill_8192", 8192)):
+        qkv = rnd(t, 48 * 128)
+        q = qkv[:, :4096].view(t, 32, 128)
+        k = qkv[:, 4096:5120].view(t, 8, 128)
+        v = qkv[:, 5120:].view(t, 8, 128)
+        positions = torch.randint(0, 2048, (t,), generator=gd, device=dev)
+        loc = torch.randperm(pages * 16 - 1, generator=gd, device=dev)[:t] + 1
+        ms = _event_time_ms(lambda: ops.qk_norm_rope_store(q, k, v, qw, kw, 1e-6, positions,
+                                                           rope, att, loc), reps)
+        nbytes = t * 128 * 2 * (32 * 2 + 8 * 2 + 8 + 16) + 16 * t
+        res = {"us": round(ms * 1e3, 2), "bytes": nbytes,
+               "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        if cpu:
+            from oracle import layer_ops as olo, norms as onorms  # the CPU baseline only
+            n = min(t, 1024)
+            qs, ks = q[:n].float().cpu(), k[:n].float().cpu()
+            qwc, kwc = qw.float().cpu(), kw.float().cpu()
+            cos, sin = olo.rope_tables(40960, 128, 1_000_000.0)
+            pos = positions[:n].cpu().numpy()
+            kcc = torch.zeros(n + 1, 8, 128)
+            lc = torch.arange(1, n + 1)
+            vs = v[:n].float().cpu()
+
+            def cpu_pass():
+                qn, kn = onorms.qk_norm_torch(qs, ks, qwc, kwc, 1e-6)
+                olo.rope(qn.numpy(), pos, cos, sin)
+                kr = torch.from_numpy(olo.rope(kn.numpy(), pos, cos, sin))
+                kcc.index_copy_(0, lc, kr)
+                kcc.index_copy_(0, lc, vs)
+            cms, threads = _cpu_median_ms(cpu_pass)
+            cbytes = n * 128 * 2 * (32 * 2 + 8 * 2 + 8 + 16) + 16 * n
+            res["cpu_baseline"] = {
+                "value": round(cbytes / (cms * 1e-3) / 1e9, 2), "unit": "GB/s", "cores": threads,
+                "kind": "port", "sample": f"{n} of the {t} tokens, torch-CPU / numpy restatement "
+                                          "(ops.rs:39-51, 84-97, base.rs:123-151), median of 3"}
+        out[name] = res
+    del kc, vc
+
+    # SiLU x mul of the prompt batch: gate_up [8192, 2 x 12288].
+    gu = rnd(8192, 2 * 12288)
+    act = torch.empty(8192, 12288, dtype=torch.bfloat16, device=dev)
+    ms = _event_time_ms(lambda: ops.silu_and_mul(gu, out=act), reps)
+    nbytes = 3 * 8192 * 12288 * 2
+    res = {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+           "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    if cpu:
+        from oracle import layer_ops as olo  # the CPU baseline only
+        sample = gu[:256].float().cpu().numpy()
+        cms = _cpu_single_ms(lambda: olo.silu_mul(sample))
+        res["cpu_baseline"] = {"value": round(3 * 256 * 12288 * 2 / (cms * 1e-3) / 1e9, 2),
+                               "unit": "GB/s", "cores": 1, "kind": "port",
+                               "sample": "256 of the 8192 rows, numpy restatement (ops.rs:53-61), "
+                                         "median of 3"}
+    out["silu_mul_8192x12288"] = res
+    del gu, act
+
+    # Decode-batch projections at 256 rows (Qwen3-8B): QKV, o_proj, gate_up + SiLU, down.
+    x = rnd(256, 12288, scale=0.5)
+    shapes = (("qkv", 6144, 4096), ("o_proj", 4096, 4096), ("gate_up_silu", 24576, 4096),
+              ("down", 4096, 12288))
+    sets = [{nm: rnd(n, kk, scale=0.02) for nm, n, kk in shapes} for _ in range(2)]
+    for nm, n, kk in shapes:
+        xs = x[:, :kk]
+        if nm == "gate_up_silu":
+            o = torch.empty(256, n // 2, dtype=torch.bfloat16, device=dev)
+            fn = lambda i, xs=xs, o=o, nm=nm: ops.decode_linear_silu_mul(xs, sets[i % 2][nm], out=o)
+        else:
+            o = torch.empty(256, n, dtype=torch.bfloat16, device=dev)
+            fn = lambda i, xs=xs, o=o, nm=nm: ops.decode_linear(xs, sets[i % 2][nm], out=o)
+        state = {"i": 0}
+
+        def step(fn=fn, state=state):
+            fn(state["i"])
+            state["i"] += 1
+        ms = _event_time_ms(step, reps)
+        wbytes = n * kk * 2
+        flops = 2 * 256 * n * kk
+        res = {"us": round(ms * 1e3, 2), "weight_bytes": wbytes,
+               "TB/s": round(wbytes / (ms * 1e-3) / 1e12, 3),
+               "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}
+        if cpu:
+            xc = xs[:16].float().cpu()
+            wc = sets[0][nm].float().cpu()
+            cms, threads = _cpu_median_ms(lambda: xc @ wc.T)
+            res["cpu_baseline"] = {"value": round(2 * 16 * n * kk / (cms * 1e-3) / 1e9, 2),
+                                   "unit": "GFLOP/s", "cores": threads, "kind": "port",
+                                   "sample": "16 of the 256 rows, torch-CPU fp32 x @ w^T "
+                                             "(linear.rs:5-7), median of 3"}
+        out[f"linear_256_{nm}"] = res
+    del sets, x
+    torch.cuda.empty_cache()
+    return out
+
+
 def norm_sections(dev, reps: int, cpu: bool = True) -> dict:
     """cfg3 norms on 8192 x 1024 hidden rows and the 8192-token packed QKV (HBM-bound), each
     with the oracle's torch-CPU restatement timed on the full rows (reported baseline)."""
@@ -707,8 +864,9 @@ def main():
     if args.only == "e2e":
         print(json.dumps({"e2e": e2e_section(dev, args)}))
         return
-    if args.only in ("prefill", "norms"):
-        fn = prefill_sections if args.only == "prefill" else norm_sections
+    if args.only in ("prefill", "norms", "serving_ops"):
+        fn = {"prefill": prefill_sections, "norms": norm_sections,
+              "serving_ops": serving_ops_section}[args.only]
         print(json.dumps({args.only: fn(dev, SECTION_REPS, cpu=not args.no_cpu_baseline)}))
         return
     w = build_workload(args.seed, dev)
@@ -822,6 +980,8 @@ def main():
     if not args.decode_only:
         result["prefill"] = prefill_sections(dev, SECTION_REPS, cpu=not args.no_cpu_baseline)
         result["norms"] = norm_sections(dev, SECTION_REPS, cpu=not args.no_cpu_baseline)
+        result["serving_ops"] = serving_ops_section(dev, SECTION_REPS,
+                                                    cpu=not args.no_cpu_baseline)
         ceil = ceilings_section(dev, w, min(reps, 50))
         ceil["decode_vs_gather"] = round(achieved / ceil["gather_2k_rows"]["GB/s"], 4)
         core = ceil["attention_core_random"]["TFLOP/s"]

@@ -23,7 +23,9 @@ import enum
 import math
 import weakref
 from dataclasses import dataclass, field
+from typing import Sequence
 
+import numpy as np
 import torch
 
 from ._native import NativeError, check, dtype_code, last_error, lib, stream_of
@@ -68,7 +70,7 @@ class AttentionSpec:
 
 @dataclass
 class DecodeHostMetadata:
-    cache_seqlens: list[int]
+    cache_seqlens: Sequence[int]    # a list, or an int32 array passed without a copy
     block_table_versions: list[int] | None = None
 
 
@@ -205,9 +207,11 @@ def prepare_decode_plan(existing: DecodePlan | None, metadata: AttentionMetadata
     host = None
     rows = 0
     if metadata.decode_host is not None:
-        values = list(metadata.decode_host.cache_seqlens)
-        rows = len(values)
-        host = (ctypes.c_int32 * max(rows, 1))(*values)
+        values = np.ascontiguousarray(metadata.decode_host.cache_seqlens, np.int32)
+        rows = values.size
+        if rows == 0:
+            raise ModelError("invalid host decode metadata")
+        host = values.ctypes.data  # ``values`` outlives the call
     handle = lib().mi355x_decode_prepare(
         existing.handle if existing else None, table.data_ptr(), table.size(0), table.size(1),
         table.stride(0), lengths.data_ptr(), spec.num_heads, spec.num_kv_heads, spec.head_dim,
@@ -342,9 +346,9 @@ class DecodeGraphState:
         self.page_size = page_size
 
     def prepare_replay(self, host: DecodeHostMetadata | None) -> None:
-        if host is not None:
-            seqlens = list(host.cache_seqlens)
-            seqlens += [1] * (self.table.size(0) - len(seqlens))  # pad rows read page 0
+        if host is not None and len(host.cache_seqlens) < self.table.size(0):
+            seqlens = np.ones(self.table.size(0), np.int32)  # pad rows read page 0
+            seqlens[:len(host.cache_seqlens)] = host.cache_seqlens
             host = DecodeHostMetadata(seqlens)
         meta = AttentionMetadata(forward_mode=BatchPhase.DECODE, decode_host=host,
                                  block_table=self.table, cache_seqlens=self.lengths)

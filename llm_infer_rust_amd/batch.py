@@ -178,29 +178,35 @@ class DecodeTables:
             return None
         if n > self.max_running_req:
             raise BatchError("request count exceeds max_running_req")
-        ids, lens, loc = [], [], []
-        ps = self.page_size
+        ps, max_len, max_blocks = self.page_size, self.max_seq_len, self.max_blocks
+        rows = self.rows
+        ids, lens, loc = [0] * n, [0] * n, [0] * n
         for r, req in enumerate(requests):
             length = req.length
-            if not 0 < length <= self.max_seq_len:
+            if not 0 < length <= max_len:
                 raise BatchError(f"request {req.uid} length {length} is outside "
-                                 f"1..={self.max_seq_len}")
-            page_index = (length - 1) // ps
-            if page_index >= len(req.page_ids):
+                                 f"1..={max_len}")
+            pages = req.page_ids
+            count = len(pages)
+            page_index, offset = divmod(length - 1, ps)
+            if page_index >= count:
                 raise BatchError(f"request {req.uid} has no writable KV page for position "
                                  f"{length - 1}")
-            slot = req.page_ids[page_index] * ps + (length - 1) % ps
+            slot = pages[page_index] * ps + offset
             if slot >= 2 ** 31:
                 raise BatchError("KV slot exceeds i32")
-            ids.append(req.input_id)
-            lens.append(length)
-            loc.append(slot)
-            self._map_row(r, req)
-        lens_a = np.asarray(lens, np.int32)
-        return DecodeBatch([req.uid for req in requests], np.asarray(ids, np.int64),
-                           lens_a.astype(np.int64) - 1, np.asarray(loc, np.int64), lens_a,
-                           self.table[:n], [row.table_version for row in self.rows[:n]],
-                           int(lens_a.max()))
+            ids[r] = req.input_id
+            lens[r] = length
+            loc[r] = slot
+            row = rows[r]
+            if (row.uid != req.uid or row.page_version != req.page_version
+                    or row.pages != (count if count < max_blocks else max_blocks)):
+                self._map_row(r, req)  # new request, changed pages, or a page appended
+        lens_a = np.array(lens, np.int32)
+        return DecodeBatch([req.uid for req in requests], np.array(ids, np.int64),
+                           lens_a.astype(np.int64) - 1, np.array(loc, np.int64), lens_a,
+                           self.table[:n], [row.table_version for row in rows[:n]],
+                           max(lens))
 
     def _map_row(self, r: int, req: DecodeRequest) -> None:
         row = self.rows[r]

@@ -158,6 +158,7 @@ class Engine:
         self.finished: list[Request] = []
         self._next_uid = 0
         self._staging = torch.empty(0, dtype=torch.int64, pin_memory=True)
+        self._staging_copy: torch.cuda.Event | None = None
         self.graphs: dict[int, _DecodeGraph] = {}
         self.stats = {"prefill_batches": 0, "decode_steps": 0, "graph_steps": 0}
         if cfg.use_graphs:
@@ -182,14 +183,34 @@ class Engine:
         if need > 0:
             req.pages.extend(self.pages.alloc(need))
 
+    def _staging_words(self, total: int) -> np.ndarray:
+        """The pinned staging block as ``total`` writable int64 words. The previous upload's
+        copy out of it is asynchronous, so wait for that copy before the block is rewritten."""
+        if self._staging_copy is not None:
+            self._staging_copy.synchronize()
+            self._staging_copy = None
+        if self._staging.numel() < total:
+            self._staging = torch.empty(max(total, 2 * self._staging.numel()), dtype=torch.int64,
+                                        pin_memory=True)
+        return self._staging.numpy()[:total]
+
+    def _send(self, total: int, dst: torch.Tensor | None = None) -> torch.Tensor:
+        """One asynchronous host-to-device copy of the first ``total`` staged words (into
+        ``dst`` when given), remembered so the next writer waits for it."""
+        src = self._staging[:total]
+        if dst is None:
+            dst = src.to(self.device, non_blocking=True)
+        else:
+            dst.copy_(src, non_blocking=True)
+        self._staging_copy = torch.cuda.Event()
+        self._staging_copy.record(torch.cuda.current_stream(self.device))
+        return dst
+
     def _pack(self, arrays) -> int:
         """Copy int32/int64 arrays into the pinned staging buffer as 8-byte words."""
         words = [_words(a) for a in arrays]
         total = sum(w.size for w in words)
-        if self._staging.numel() < total:
-            self._staging = torch.empty(max(total, 2 * self._staging.numel()), dtype=torch.int64,
-                                        pin_memory=True)
-        host = self._staging.numpy()
+        host = self._staging_words(total)
         off = 0
         for w in words:
             host[off:off + w.size] = w
@@ -198,9 +219,7 @@ class Engine:
 
     def _upload(self, *arrays: np.ndarray) -> list[torch.Tensor]:
         """One pinned staging block, one host-to-device copy; returns typed device views."""
-        total = self._pack(arrays)
-        dev = self._staging[:total].to(self.device, non_blocking=True)
-        return _views(dev, arrays)
+        return _views(self._send(self._pack(arrays)), arrays)
 
     # ------------------------------------------------------------------ prefill
     def _select_prefill(self) -> list[tuple[Request, int]]:
@@ -262,10 +281,12 @@ class Engine:
                 and not r.finished()]
 
     def _decode_batch(self, rows: list[Request]) -> DecodeBatch:
+        ps = self.page_size
         reqs = []
         for req in rows:
-            length = req.cached_len + 1   # the fed token sits at position cached_len
-            self._ensure_pages(req, length)
+            length = req.cursor + len(req.output)  # cached_len + 1: the fed token's position + 1
+            if -(-length // ps) > len(req.pages):
+                self._ensure_pages(req, length)
             reqs.append(DecodeRequest(req.uid, length, req.output[-1], req.pages))
         return self.tables.prepare(reqs)
 
@@ -293,13 +314,15 @@ class Engine:
         pending = self.sampler.defer_batch(logits, [r.params for r in rows])
         ids = pending.finish()
         now = time.perf_counter()
+        done = []
         for req, tok in zip(rows, ids):
-            req.output.append(int(tok))
+            req.output.append(tok)
             if req.first_token_time is None:
                 req.first_token_time = now
             if req.finished():
                 req.finish_time = now
-        for req in [r for r in rows if r.finished()]:
+                done.append(req)
+        for req in done:
             self.running.remove(req)
             self.finished.append(req)
             self.pages.release(req.pages)
@@ -348,19 +371,25 @@ class Engine:
             self.graphs[bs] = g
 
     def _replay(self, g: _DecodeGraph, b: DecodeBatch) -> None:
-        n, bs = b.input_ids.size, g.bs
-        pad = bs - n
-        # Pad rows (``graph.rs:285-320``): token 1 at position 0, the reserved slot 0, length 1,
-        # every block-table column page 0.
-        table = np.zeros((bs, self.cols), np.int32)
+        n, bs, cols = b.input_ids.size, g.bs, self.cols
+        # The graph's input block is staged in its own layout (``_DecodeGraph``: three int64
+        # runs, then the int32 lengths and block table) and sent with one copy. Pad rows
+        # (``graph.rs:285-320``): token 1 at position 0, the reserved slot 0, length 1, every
+        # block-table column page 0.
+        len_words, tab_words = (bs + 1) // 2, (bs * cols + 1) // 2
+        host = self._staging_words(3 * bs + len_words + tab_words)
+        for k, (src, pad) in enumerate(((b.input_ids, 1), (b.positions, 0), (b.write_loc, 0))):
+            run = host[k * bs:(k + 1) * bs]
+            run[:n] = src
+            run[n:] = pad
+        lens = host[3 * bs:3 * bs + len_words].view(np.int32)[:bs]
+        lens[:n] = b.cache_seqlens
+        lens[n:] = 1
+        table = host[3 * bs + len_words:].view(np.int32)[:bs * cols].reshape(bs, cols)
         table[:n] = b.block_table
-        arrays = (np.concatenate([b.input_ids, np.ones(pad, np.int64)]),
-                  np.concatenate([b.positions, np.zeros(pad, np.int64)]),
-                  np.concatenate([b.write_loc, np.zeros(pad, np.int64)]),
-                  np.concatenate([b.cache_seqlens, np.ones(pad, np.int32)]), table)
-        total = self._pack(arrays)
-        g.block.copy_(self._staging[:total], non_blocking=True)  # one copy into the graph inputs
-        g.state.prepare_replay(DecodeHostMetadata(b.cache_seqlens.tolist()))
+        table[n:] = 0
+        self._send(host.size, g.block)
+        g.state.prepare_replay(DecodeHostMetadata(lens))
         g.graph.replay()
 
     # ------------------------------------------------------------------ loop

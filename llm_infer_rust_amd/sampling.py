@@ -89,6 +89,7 @@ class Sampler:
     def __init__(self, seed: int = 0):
         self.manual_seed(seed)
         self._param_key: tuple | None = None
+        self._param_objs: tuple | None = None
         self._params: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None
 
     def manual_seed(self, seed: int) -> None:
@@ -96,8 +97,17 @@ class Sampler:
         self.offset = 0
 
     def _device_params(self, params_list, device: torch.device):
+        # A decode step usually passes the very objects of the previous step (each running
+        # request keeps its SamplingParams, which are frozen): reuse the device arrays after
+        # an identity check instead of normalising every row again on the host.
+        objs = self._param_objs
+        if (objs is not None and self._param_key is not None and self._param_key[0] == device
+                and len(objs) == len(params_list)
+                and all(a is b for a, b in zip(params_list, objs))):
+            return self._params
         normalized = [p.normalized() for p in params_list]
         key = (device, tuple((p.temperature, p.top_k, p.top_p) for p in normalized))
+        self._param_objs = tuple(params_list)
         if key != self._param_key:
             n = len(normalized)
             host = torch.empty(3 * n, dtype=torch.float32, pin_memory=True)
