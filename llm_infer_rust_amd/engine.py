@@ -136,6 +136,25 @@ class _DecodeGraph:
         self.batch = None
 
 
+@dataclass
+class _Ahead:
+    """A decode step staged one step early: its rows, their lengths, the graph bucket and the
+    staged words (the input-token run still to be written once the tokens are known)."""
+
+    uids: list[int]
+    lengths: list[int]
+    graph: _DecodeGraph
+    host: np.ndarray
+    lens: np.ndarray
+
+    def matches(self, rows: list, graph: _DecodeGraph) -> bool:
+        """The staged step is the one to run: same graph, same rows in the same order, each
+        at the length it was staged for (pages only grow, and the staging ensured them)."""
+        return (graph is self.graph and len(rows) == len(self.uids)
+                and all(r.uid == u and r.cursor + len(r.output) == n
+                        for r, u, n in zip(rows, self.uids, self.lengths)))
+
+
 class Engine:
     def __init__(self, model: Qwen3Model, config: EngineConfig | None = None):
         self.model = model
@@ -159,8 +178,11 @@ class Engine:
         self._next_uid = 0
         self._staging = torch.empty(0, dtype=torch.int64, pin_memory=True)
         self._staging_copy: torch.cuda.Event | None = None
+        self._ahead: _Ahead | None = None           # next decode step, staged while this one runs
+        self._pending_rows: list[Request] | None = None
         self.graphs: dict[int, _DecodeGraph] = {}
-        self.stats = {"prefill_batches": 0, "decode_steps": 0, "graph_steps": 0}
+        self.stats = {"prefill_batches": 0, "decode_steps": 0, "graph_steps": 0,
+                      "ahead_steps": 0}
         if cfg.use_graphs:
             self.capture_graphs()
 
@@ -186,6 +208,7 @@ class Engine:
     def _staging_words(self, total: int) -> np.ndarray:
         """The pinned staging block as ``total`` writable int64 words. The previous upload's
         copy out of it is asynchronous, so wait for that copy before the block is rewritten."""
+        self._ahead = None  # a step staged ahead lives in this block: rewriting it voids that
         if self._staging_copy is not None:
             self._staging_copy.synchronize()
             self._staging_copy = None
@@ -292,13 +315,20 @@ class Engine:
 
     def _run_decode(self, rows: list[Request]) -> None:
         n = len(rows)
-        b = self._decode_batch(rows)
         graph = self._graph_for(n)
+        ahead, self._ahead = self._ahead, None
         if graph is not None:
-            self._replay(graph, b)
+            if ahead is not None and ahead.matches(rows, graph):
+                host, lens = ahead.host, ahead.lens
+                host[:n] = [req.output[-1] for req in rows]  # the tokens sampled last step
+                self.stats["ahead_steps"] += 1
+            else:
+                host, lens = self._stage_replay(graph, self._decode_batch(rows))
+            self._launch_replay(graph, host, lens)
             logits = graph.logits[:n]
             self.stats["graph_steps"] += 1
         else:
+            b = self._decode_batch(rows)
             ids_d, pos_d, loc_d, lens_d, table_d = self._upload(
                 b.input_ids, b.positions, b.write_loc, b.cache_seqlens, b.block_table)
             meta = AttentionMetadata(BatchPhase.DECODE, decode_host=DecodeHostMetadata(
@@ -308,10 +338,36 @@ class Engine:
             logits = self.model.forward(ids_d, pos_d, batch, loc_d)
             del batch
         self.stats["decode_steps"] += 1
+        if graph is not None:
+            self._pending_rows = rows  # the sampler's wait runs the next step's host work
         self._sample_and_commit(logits, rows)
+
+    def _prepare_ahead(self, rows: list[Request]) -> None:
+        """While this step runs on the GPU: stage the next decode step for the rows that will
+        still decode (this step's sampling cannot end them by length; an end-of-sequence token
+        or a prefill that changes the row set discards the staging, see ``_Ahead.matches``)."""
+        if self.waiting or any(r.cursor < r.prompt.size for r in self.running):
+            return  # the next step starts with a prefill and changes the decode rows
+        nxt = [r for r in rows if len(r.output) + 1 < r.params.max_tokens]
+        graph = self._graph_for(len(nxt)) if nxt else None
+        if graph is None:
+            return
+        ps = self.page_size
+        reqs, lengths = [], []
+        for req in nxt:
+            length = req.cursor + len(req.output) + 1  # after this step's token is appended
+            if -(-length // ps) > len(req.pages):
+                self._ensure_pages(req, length)
+            reqs.append(DecodeRequest(req.uid, length, 0, req.pages))
+            lengths.append(length)
+        host, lens = self._stage_replay(graph, self.tables.prepare(reqs))
+        self._ahead = _Ahead([r.uid for r in nxt], lengths, graph, host, lens)
 
     def _sample_and_commit(self, logits: torch.Tensor, rows: list[Request]) -> None:
         pending = self.sampler.defer_batch(logits, [r.params for r in rows])
+        ahead_rows, self._pending_rows = self._pending_rows, None
+        if ahead_rows is not None:
+            self._prepare_ahead(ahead_rows)
         ids = pending.finish()
         now = time.perf_counter()
         done = []
@@ -370,12 +426,12 @@ class Engine:
             torch.cuda.synchronize(self.device)
             self.graphs[bs] = g
 
-    def _replay(self, g: _DecodeGraph, b: DecodeBatch) -> None:
+    def _stage_replay(self, g: _DecodeGraph, b: DecodeBatch) -> tuple[np.ndarray, np.ndarray]:
+        """Write a decode batch into the pinned staging block in the graph's input layout
+        (``_DecodeGraph``: three int64 runs, then the int32 lengths and block table). Pad rows
+        (``graph.rs:285-320``): token 1 at position 0, the reserved slot 0, length 1, every
+        block-table column page 0. Returns the staged words and the staged lengths."""
         n, bs, cols = b.input_ids.size, g.bs, self.cols
-        # The graph's input block is staged in its own layout (``_DecodeGraph``: three int64
-        # runs, then the int32 lengths and block table) and sent with one copy. Pad rows
-        # (``graph.rs:285-320``): token 1 at position 0, the reserved slot 0, length 1, every
-        # block-table column page 0.
         len_words, tab_words = (bs + 1) // 2, (bs * cols + 1) // 2
         host = self._staging_words(3 * bs + len_words + tab_words)
         for k, (src, pad) in enumerate(((b.input_ids, 1), (b.positions, 0), (b.write_loc, 0))):
@@ -388,6 +444,10 @@ class Engine:
         table = host[3 * bs + len_words:].view(np.int32)[:bs * cols].reshape(bs, cols)
         table[:n] = b.block_table
         table[n:] = 0
+        return host, lens
+
+    def _launch_replay(self, g: _DecodeGraph, host: np.ndarray, lens: np.ndarray) -> None:
+        """One copy into the graph's inputs, the host-length re-plan, the replay."""
         self._send(host.size, g.block)
         g.state.prepare_replay(DecodeHostMetadata(lens))
         g.graph.replay()

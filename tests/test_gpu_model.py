@@ -206,3 +206,40 @@ def test_chunked_long_prompt_uses_split_prefill(gpu):
     assert eng.stats["prefill_batches"] == 5 and max(seen) > 0, seen
     assert len(req.output) == 4
     check_teacher_forced(oracle, prompt, req.output, tol=0.05)
+
+
+def test_decode_staged_ahead_matches_unstaged(gpu):
+    """The graph path stages each decode step while the previous one runs and uses it only
+    when the rows, their order and lengths are the ones it was staged for. Greedy tokens with
+    staging on must equal those with staging off (same graph bucket, so the same kernels), and
+    a request that ends on its end-of-sequence token must discard the staged step: it stops
+    right after that token and the other requests carry on unchanged."""
+    model, _ = build(TINY, 12, gpu)
+    rng = np.random.default_rng(13)
+    prompts = [rng.integers(0, TINY.vocab_size, n) for n in (9, 30, 21)]
+
+    def run(eos=None, staged=True):
+        eng = Engine(model, EngineConfig(max_running_req=4, max_seq_len=128, seed=3,
+                                         graph_batch_sizes=(4,)))
+        if not staged:
+            eng._prepare_ahead = lambda rows: None
+        reqs = [eng.add_request(p, SamplingParams(max_tokens=10),
+                                eos_token_id=eos if i == 0 else None)
+                for i, p in enumerate(prompts)]
+        eng.run_until_complete()
+        out = [list(r.output) for r in reqs]
+        stats = dict(eng.stats)
+        del eng
+        torch.cuda.synchronize()
+        return out, stats
+
+    plain, st_off = run(staged=False)
+    staged, st_on = run()
+    assert st_off["ahead_steps"] == 0 and st_on["ahead_steps"] > 0
+    assert staged == plain
+    # End request 0 on the token it emits at step 4 (its first occurrence there).
+    stop = next(i for i in range(3, 9) if plain[0][i] not in plain[0][:i])
+    cut, st_eos = run(eos=plain[0][stop])
+    assert cut[0] == plain[0][:stop + 1]
+    assert cut[1:] == plain[1:]
+    assert st_eos["ahead_steps"] > 0
