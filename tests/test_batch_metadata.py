@@ -143,3 +143,27 @@ def test_compacting_rows_keeps_each_request_mapping():
 def test_request_count_is_bounded():
     with pytest.raises(BatchError, match="max_running_req"):
         _tables().prepare([_running(i, [1], [i + 1]) for i in range(3)])
+
+
+def test_staged_decode_step_matches_only_its_rows_and_lengths():
+    """A decode step staged one step early (``engine._Ahead``) is used only for the same graph,
+    the same rows in the same order, each at the length it was staged for."""
+    from types import SimpleNamespace
+
+    import numpy as np
+
+    from llm_infer_rust_amd.engine import _Ahead
+
+    def row(uid, cursor, outputs):
+        return SimpleNamespace(uid=uid, cursor=cursor, output=[7] * outputs)
+
+    graph, other = object(), object()
+    staged = _Ahead([3, 5], [12, 21], graph, np.zeros(4, np.int64), np.zeros(2, np.int32))
+    rows = [row(3, 10, 2), row(5, 20, 1)]
+    assert staged.matches(rows, graph)
+    assert not staged.matches(rows, other)                        # another graph bucket
+    assert not staged.matches(rows[::-1], graph)                  # order changed
+    assert not staged.matches(rows[:1], graph)                    # a row ended
+    assert not staged.matches(rows + [row(9, 4, 1)], graph)       # a row joined
+    assert not staged.matches([row(3, 10, 3), rows[1]], graph)    # length moved on
+    assert not staged.matches([row(4, 10, 2), rows[1]], graph)    # another request
