@@ -353,13 +353,15 @@ class Engine:
         if graph is None:
             return
         ps = self.page_size
-        reqs, lengths = [], []
-        for req in nxt:
-            length = req.cursor + len(req.output) + 1  # after this step's token is appended
+        lengths = [req.cursor + len(req.output) + 1 for req in nxt]  # after this step's token
+        need = sum(max(0, -(-n // ps) - len(req.pages)) for req, n in zip(nxt, lengths))
+        if need > len(self.pages.free):
+            return  # the next step raises "out of KV-cache pages" itself, after this commit
+        reqs = []
+        for req, length in zip(nxt, lengths):
             if -(-length // ps) > len(req.pages):
                 self._ensure_pages(req, length)
             reqs.append(DecodeRequest(req.uid, length, 0, req.pages))
-            lengths.append(length)
         host, lens = self._stage_replay(graph, self.tables.prepare(reqs))
         self._ahead = _Ahead([r.uid for r in nxt], lengths, graph, host, lens)
 
