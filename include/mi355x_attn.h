@@ -273,6 +273,23 @@ const char* mi355x_linear_add_rms_norm(const void* x, int64_t ldx, const void* w
                                        int64_t K, void* workspace, int64_t workspace_bytes,
                                        int32_t cus, int64_t dtype, void* stream);
 
+/* The QKV projection fused with the qk_norm -> rope -> K/V store pass that reads it
+ * (decode batches): qkv[M, (Hq + 2 Hkv) * 128] = x . w^T, then mi355x_qk_norm_rope_store
+ * on its q, k and v head views (token stride ldo, head stride 128) with every stage on
+ * (norm weights, positions and a cache are required). When the product is split along K
+ * the pass sums the fp32 partials itself (split order, rounded once) instead of a separate
+ * reduce launch, and writes the v rows into qkv too, so qkv and the cache equal
+ * mi355x_linear (library tiling) followed by mi355x_qk_norm_rope_store bit for bit.
+ * Workspace as for mi355x_linear with config = splits = -1 (N = (Hq + 2 Hkv) * 128).
+ * Replaces linear.rs:5-7 followed by model.rs:478-514 (fused_ops.cu, base.rs:62-152). */
+const char* mi355x_linear_qk_norm_rope_store(
+    const void* x, int64_t ldx, const void* w, int64_t ldw, void* qkv, int64_t ldo, int64_t M,
+    int64_t K, int64_t q_heads, int64_t k_heads, void* workspace, int64_t workspace_bytes,
+    int32_t cus, const void* q_weight, const void* k_weight, const int64_t* positions,
+    const float* cos, const float* sin, int64_t max_positions, void* k_cache, void* v_cache,
+    const void* loc, bool index64, int64_t capacity, int64_t reserved, int32_t* error_count,
+    double eps, int dtype, void* stream);
+
 /* A gate_up projection fused with SiLU x mul (the MLP's first two steps):
  *   y = x . w^T with w = [gate rows (width); up rows (width)] of [2 width, K],
  *   out[m, j] = round(silu(g) * u), g = round(y[m, j]), u = round(y[m, width + j]),

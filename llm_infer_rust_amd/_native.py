@@ -77,6 +77,13 @@ SIGNATURES: dict[str, tuple] = {
                                              c_void_p, c_void_p, c_bool, c_i64, c_i64, c_void_p,
                                              c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                              c_i64, c_i64, c_i64, c_double, c_int, c_void_p]),
+    "mi355x_linear_qk_norm_rope_store": (c_char_p, [c_void_p, c_i64, c_void_p, c_i64,
+                                                    c_void_p, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                                    c_void_p, c_i64, c_i32, c_void_p, c_void_p,
+                                                    c_void_p, c_void_p, c_void_p, c_i64,
+                                                    c_void_p, c_void_p, c_void_p, c_bool, c_i64,
+                                                    c_i64, c_void_p, c_double, c_int,
+                                                    c_void_p]),
     "mi355x_silu_mul": (c_char_p, [c_void_p, c_void_p, c_i64, c_i64, c_int, c_void_p]),
     "mi355x_linear": (c_char_p, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_i64, c_i64,
                                  c_i64, c_i64, c_void_p, c_i64, c_i32, c_i32, c_i32, c_i64,

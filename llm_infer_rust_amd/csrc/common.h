@@ -218,4 +218,12 @@ __device__ __forceinline__ void st128(void* p, const uint4& v) {
   *reinterpret_cast<uint4*>(p) = v;
 }
 
+// The decode-batch projection launcher of linear.hip (validation, tiling, split-K). With
+// leave_partials the fp32 partials [splits][M][N] stay in `workspace` unreduced and
+// *splits_used says how many there are (1: `out` holds the product).
+const char* run_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, void* out,
+                       int64_t ldo, int64_t M, int64_t N, int64_t K, void* workspace,
+                       int64_t workspace_bytes, int32_t cus, int32_t config, int32_t splits,
+                       int64_t dtype, bool leave_partials, int* splits_used, hipStream_t s);
+
 }  // namespace mi355x

@@ -52,10 +52,40 @@ struct HeadArgs {
   int64_t qs0, qs1, ks0, ks1, vs0, vs1;
   int64_t max_positions, capacity, reserved;
   float eps;
+  // Partials mode: q/k/v rows are the sum of split-K fp32 partials [splits][tokens][ld]
+  // (ld = (q_heads + 2 k_heads) * 128), rounded once, and v is written to v_out as well.
+  const float* part;
+  int64_t part_ld, part_plane;
+  int32_t part_splits;
+  uint16_t* v_out;
+  int64_t vos0, vos1;
 };
 
+// One row's 8 columns from the split-K partials: split 0 plus each later split in order (the
+// order linear_reduce adds them), rounded once.
+template <int DT>
+__device__ __forceinline__ uint4 partial_row8(const HeadArgs& a, int64_t token, int64_t col) {
+  const float* p = a.part + token * a.part_ld + col;
+  float4 lo = *reinterpret_cast<const float4*>(p);
+  float4 hi = *reinterpret_cast<const float4*>(p + 4);
+  for (int s = 1; s < a.part_splits; ++s) {
+    const float4 x = *reinterpret_cast<const float4*>(p + s * a.part_plane);
+    const float4 y = *reinterpret_cast<const float4*>(p + s * a.part_plane + 4);
+    lo.x += x.x;
+    lo.y += x.y;
+    lo.z += x.z;
+    lo.w += x.w;
+    hi.x += y.x;
+    hi.y += y.y;
+    hi.z += y.z;
+    hi.w += y.w;
+  }
+  const float f[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  return pack8<DT>(f);
+}
+
 // One 16-lane group per (token, head) row, q heads first then k heads.
-template <int DT, bool NORM, bool ROPE, bool STORE, typename Index>
+template <int DT, bool NORM, bool ROPE, bool STORE, typename Index, bool PART = false>
 __global__ __launch_bounds__(256) void head_rows_kernel(HeadArgs a) {
   const int lane = threadIdx.x & 15;
   const int64_t per = a.q_heads + a.k_heads;
@@ -68,7 +98,17 @@ __global__ __launch_bounds__(256) void head_rows_kernel(HeadArgs a) {
   uint16_t* ptr = is_q ? a.q + token * a.qs0 + h * a.qs1 : a.k + token * a.ks0 + kh * a.ks1;
   ptr += lane * 8;
 
-  uint4 packed = ld128(ptr);
+  uint4 packed;
+  uint4 v_packed = make_uint4(0, 0, 0, 0);
+  if constexpr (PART) {
+    packed = partial_row8<DT>(a, token, h * kHeadDim + lane * 8);
+    if (!is_q) {  // the v row of this kv head, kept in the packed output as the reduce would
+      v_packed = partial_row8<DT>(a, token, (a.q_heads + a.k_heads + kh) * kHeadDim + lane * 8);
+      st128(a.v_out + token * a.vos0 + kh * a.vos1 + lane * 8, v_packed);
+    }
+  } else {
+    packed = ld128(ptr);
+  }
   if constexpr (NORM) {
     float x[8];
     unpack8<DT>(packed, x);
@@ -124,7 +164,7 @@ __global__ __launch_bounds__(256) void head_rows_kernel(HeadArgs a) {
     if (slot == a.reserved) return;
     const int64_t dst = (slot * a.k_heads + kh) * kHeadDim + lane * 8;
     st128(a.kc + dst, packed);
-    st128(a.vc + dst, ld128(a.v + token * a.vs0 + kh * a.vs1 + lane * 8));
+    st128(a.vc + dst, PART ? v_packed : ld128(a.v + token * a.vs0 + kh * a.vs1 + lane * 8));
   }
 }
 
@@ -156,6 +196,15 @@ template <int DT, bool NORM, bool ROPE, bool STORE>
 void launch_rows(const HeadArgs& a, bool index64, hipStream_t s) {
   const int64_t rows = a.tokens * (a.q_heads + a.k_heads);
   const dim3 grid(static_cast<uint32_t>((rows + 15) / 16));
+  if (a.part) {  // the fused QKV path always normalises, rotates and stores
+    if constexpr (NORM && ROPE && STORE) {
+      if (index64)
+        head_rows_kernel<DT, true, true, true, int64_t, true><<<grid, dim3(256), 0, s>>>(a);
+      else
+        head_rows_kernel<DT, true, true, true, int32_t, true><<<grid, dim3(256), 0, s>>>(a);
+    }
+    return;
+  }
   if (index64)
     head_rows_kernel<DT, NORM, ROPE, STORE, int64_t><<<grid, dim3(256), 0, s>>>(a);
   else
@@ -258,14 +307,17 @@ extern "C" const char* mi355x_rope(void* q, void* k, const int64_t* positions, c
   return launch_status("mi355x_rope");
 }
 
-extern "C" const char* mi355x_qk_norm_rope_store(
+namespace {
+// The QK-norm -> RoPE -> K/V store pass; with `part` its q/k/v rows come from split-K
+// partials (see HeadArgs) and v is also written to `v_out` (same strides as v).
+const char* qk_rows_impl(
     void* q, void* k, const void* v, const void* q_weight, const void* k_weight,
     const int64_t* positions, const float* cos, const float* sin, int64_t max_positions,
     void* k_cache, void* v_cache, const void* loc, bool index64, int64_t capacity,
     int64_t reserved, int32_t* error_count, int64_t tokens, int64_t q_heads, int64_t k_heads,
     int64_t width, int64_t q_token_stride, int64_t q_head_stride, int64_t k_token_stride,
     int64_t k_head_stride, int64_t v_token_stride, int64_t v_head_stride, double eps, int dtype,
-    void* stream) {
+    void* stream, const float* part, int32_t part_splits) {
   if (tokens < 0 || q_heads < 0 || k_heads < 0 || max_positions < 0 || capacity < 0)
     return set_error("mi355x_qk_norm_rope_store: bad shape");
   if (width != kHeadDim) return set_error("mi355x_qk_norm_rope_store: width must be 128");
@@ -308,6 +360,17 @@ extern "C" const char* mi355x_qk_norm_rope_store(
   a.capacity = capacity;
   a.reserved = reserved;
   a.eps = static_cast<float>(eps);
+  if (part) {
+    if (!(norm && rope && store) || part_splits < 2 || !aligned(part, 16))
+      return set_error("mi355x_linear_qk_norm_rope_store: needs norm weights, positions and a cache");
+    a.part = part;
+    a.part_splits = part_splits;
+    a.part_ld = (q_heads + 2 * k_heads) * kHeadDim;
+    a.part_plane = tokens * a.part_ld;
+    a.v_out = static_cast<uint16_t*>(const_cast<void*>(v));
+    a.vos0 = v_token_stride;
+    a.vos1 = v_head_stride;
+  }
   bool ok = head_views_vectorisable(a);
   if (norm) ok = ok && aligned(q_weight, 16) && aligned(k_weight, 16);
   if (rope) ok = ok && aligned(cos, 16) && aligned(sin, 16);
@@ -323,6 +386,48 @@ extern "C" const char* mi355x_qk_norm_rope_store(
   else
     launch_rows_dt<1>(a, norm, rope, store, index64, s);
   return launch_status("mi355x_qk_norm_rope_store");
+}
+}  // namespace
+
+extern "C" const char* mi355x_qk_norm_rope_store(
+    void* q, void* k, const void* v, const void* q_weight, const void* k_weight,
+    const int64_t* positions, const float* cos, const float* sin, int64_t max_positions,
+    void* k_cache, void* v_cache, const void* loc, bool index64, int64_t capacity,
+    int64_t reserved, int32_t* error_count, int64_t tokens, int64_t q_heads, int64_t k_heads,
+    int64_t width, int64_t q_token_stride, int64_t q_head_stride, int64_t k_token_stride,
+    int64_t k_head_stride, int64_t v_token_stride, int64_t v_head_stride, double eps, int dtype,
+    void* stream) {
+  return qk_rows_impl(q, k, v, q_weight, k_weight, positions, cos, sin, max_positions, k_cache,
+                      v_cache, loc, index64, capacity, reserved, error_count, tokens, q_heads,
+                      k_heads, width, q_token_stride, q_head_stride, k_token_stride,
+                      k_head_stride, v_token_stride, v_head_stride, eps, dtype, stream, nullptr,
+                      0);
+}
+
+extern "C" const char* mi355x_linear_qk_norm_rope_store(
+    const void* x, int64_t ldx, const void* w, int64_t ldw, void* qkv, int64_t ldo, int64_t M,
+    int64_t K, int64_t q_heads, int64_t k_heads, void* workspace, int64_t workspace_bytes,
+    int32_t cus, const void* q_weight, const void* k_weight, const int64_t* positions,
+    const float* cos, const float* sin, int64_t max_positions, void* k_cache, void* v_cache,
+    const void* loc, bool index64, int64_t capacity, int64_t reserved, int32_t* error_count,
+    double eps, int dtype, void* stream) {
+  if (M <= 0 || q_heads <= 0 || k_heads <= 0 || ldo % 8 || !qkv || !aligned(qkv, 16))
+    return set_error("mi355x_linear_qk_norm_rope_store: bad shape");
+  if (!q_weight || !k_weight || !positions || !k_cache)
+    return set_error("mi355x_linear_qk_norm_rope_store: needs norm weights, positions and a cache");
+  const int64_t N = (q_heads + 2 * k_heads) * kHeadDim;
+  if (ldo < N) return set_error("mi355x_linear_qk_norm_rope_store: ldo < (Hq + 2 Hkv) * 128");
+  auto s = static_cast<hipStream_t>(stream);
+  int used = 1;
+  if (const char* e = run_linear(x, ldx, w, ldw, qkv, ldo, M, N, K, workspace, workspace_bytes,
+                                 cus, -1, -1, dtype, true, &used, s))
+    return e;
+  auto* base = static_cast<uint16_t*>(qkv);
+  return qk_rows_impl(base, base + q_heads * kHeadDim, base + (q_heads + k_heads) * kHeadDim,
+                      q_weight, k_weight, positions, cos, sin, max_positions, k_cache, v_cache,
+                      loc, index64, capacity, reserved, error_count, M, q_heads, k_heads,
+                      kHeadDim, ldo, kHeadDim, ldo, kHeadDim, ldo, kHeadDim, eps, dtype, stream,
+                      used > 1 ? static_cast<const float*>(workspace) : nullptr, used);
 }
 
 extern "C" const char* mi355x_silu_mul(const void* gate_up, void* out, int64_t tokens,

@@ -476,9 +476,9 @@ extern "C" int64_t mi355x_linear_workspace_bytes(int64_t M, int64_t N, int64_t K
 }
 
 namespace mi355x {
-namespace {
-// Validates, picks the tiling and launches the projection. With `fuse_out_partials` the
-// split-K partials are left in the workspace (no reduce) and `*splits_used` tells how many.
+// Validates, picks the tiling and launches the projection. With `leave_partials` the
+// split-K partials are left in the workspace (no reduce) and `*splits_used` tells how many
+// (1: the product went straight to `out`). Shared with the fused QKV pass in layer_ops.hip.
 const char* run_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, void* out,
                        int64_t ldo, int64_t M, int64_t N, int64_t K, void* workspace,
                        int64_t workspace_bytes, int32_t cus, int32_t config, int32_t splits,
@@ -532,7 +532,6 @@ const char* run_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, v
   }
   return nullptr;
 }
-}  // namespace
 }  // namespace mi355x
 
 extern "C" const char* mi355x_linear(const void* x, int64_t ldx, const void* w, int64_t ldw,

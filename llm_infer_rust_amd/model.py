@@ -12,8 +12,9 @@ Follows the reference layer sequence (``src/models/qwen3/model.rs:155-534``):
     logits = add_rms_norm(hidden, residual)[logits_indices] W_lm^T
 
 For decode batches (at most 256 rows) the QKV, o_proj and down projections run on this
-library's projection kernel (o_proj and down fused with the residual RMSNorm that follows
-them) and gate_up runs fused with SiLU x mul; prefill-sized products and the lm_head are
+library's projection kernel (QKV with its split-K partials summed inside the QK-norm/RoPE/
+store pass, o_proj and down fused with the residual RMSNorm that follows them) and gate_up runs
+fused with SiLU x mul; prefill-sized products and the lm_head are
 library GEMMs (torch -> hipBLASLt). Everything around them is this library's HIP code. Configuration fields and defaults follow ``src/models/qwen3/config.rs:9-42``.
 """
 from __future__ import annotations
@@ -182,12 +183,12 @@ class Qwen3Model:
         x = ops.rms_norm(hidden, self.layers[0].input_layernorm, eps)
         n_layers = len(self.layers)
         for i, layer in enumerate(self.layers):
-            qkv = ops.linear(x, layer.qkv_proj)
+            qkv = ops.linear_qk_norm_rope_store(x, layer.qkv_proj, hq, hkv, layer.q_norm,
+                                                layer.k_norm, eps, positions, self.rope,
+                                                layer.base_attention, write_loc)
             q = qkv[:, : hq * d].view(t, hq, d)
             k = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
             v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
-            ops.qk_norm_rope_store(q, k, v, layer.q_norm, layer.k_norm, eps, positions,
-                                   self.rope, layer.base_attention, write_loc)
             attn = attention_batch.forward(q, k, v, layer.base_attention)
             # o_proj + post-attention norm, down + the next layer's input norm (the final
             # norm after the last layer): each a projection fused with its residual RMSNorm.

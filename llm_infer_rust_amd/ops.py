@@ -212,6 +212,61 @@ def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         stream_of(q)), "qk_norm_rope_store")
 
 
+def linear_qk_norm_rope_store(x: torch.Tensor, weight: torch.Tensor, q_heads: int,
+                              k_heads: int, q_weight: torch.Tensor, k_weight: torch.Tensor,
+                              eps: float, positions: torch.Tensor, rope_tables: HalfSplitRope,
+                              attention, write_loc: torch.Tensor | None) -> torch.Tensor:
+    """The decoder layer's ``qkv = linear(x, W_qkv)`` followed by ``qk_norm_rope_store`` on its
+    q/k/v head views; returns ``qkv`` ``[T, (Hq + 2 Hkv) 128]``. Decode-sized products with a
+    bound cache run as one projection plus one pass that also sums the split-K partials
+    (``mi355x_linear_qk_norm_rope_store``, bit-identical to the two steps); everything else
+    runs the two steps."""
+    m, k = (x.shape if x.dim() == 2 else (0, 0))
+    n = weight.size(0)
+    d = 128
+    fused = (x.is_cuda and x.dim() == 2 and x.stride(1) == 1 and x.stride(0) % 8 == 0
+             and weight.is_contiguous() and n == (q_heads + 2 * k_heads) * d
+             and uses_decode_kernel(m, n, k) and attention is not None
+             and write_loc is not None and attention.is_bound() and rope_tables is not None)
+    if not fused:
+        qkv = linear(x, weight)
+        t = qkv.size(0)
+        qk_norm_rope_store(qkv[:, :q_heads * d].view(t, q_heads, d),
+                           qkv[:, q_heads * d:(q_heads + k_heads) * d].view(t, k_heads, d),
+                           qkv[:, (q_heads + k_heads) * d:].view(t, k_heads, d), q_weight,
+                           k_weight, eps, positions, rope_tables, attention, write_loc)
+        return qkv
+    _require_device(x, "linear_qk_norm_rope_store")
+    dt = dtype_code(x)
+    if weight.dtype != x.dtype or weight.device != x.device or weight.size(1) != k:
+        raise NativeError("invalid linear operands: expected x [M, K] and weight [N, K]")
+    qkv = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    q_view = qkv[:, :q_heads * d].view(m, q_heads, d)
+    _check_weight(q_view, q_weight, d)
+    _check_weight(q_view, k_weight, d)
+    cos, sin, max_pos = rope_tables.cos, rope_tables.sin, rope_tables.max_positions
+    _check_positions(q_view, positions, cos, sin)
+    kc, vc = attention.cache_tensors()
+    if kc.size(2) != k_heads or kc.size(3) != d or kc.dtype != x.dtype:
+        raise NativeError("K/V input head shape does not match the bound cache")
+    if (write_loc.dim() != 1 or write_loc.numel() != m or not write_loc.is_contiguous()
+            or write_loc.dtype not in (torch.int32, torch.int64) or write_loc.device != x.device):
+        raise NativeError("invalid KV store locations")
+    cus = _native.device_cus(x.device)
+    need = lib().mi355x_linear_workspace_bytes(m, n, k, cus, -1, -1)
+    ws = torch.empty(max(int(need), 16), dtype=torch.uint8, device=x.device) if need else None
+    check(lib().mi355x_linear_qk_norm_rope_store(
+        x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), qkv.data_ptr(), n, m, k,
+        q_heads, k_heads, None if ws is None else ws.data_ptr(), int(need), cus,
+        q_weight.data_ptr(), k_weight.data_ptr(), positions.data_ptr(), cos.data_ptr(),
+        sin.data_ptr(), max_pos, kc.data_ptr(), vc.data_ptr(), write_loc.data_ptr(),
+        write_loc.dtype == torch.int64, kc.size(0) * kc.size(1),
+        attention.reserved_write_slot(),
+        None if attention.error_word() is None else attention.error_word().data_ptr(), float(eps), dt,
+        stream_of(x)), "linear_qk_norm_rope_store")
+    return qkv
+
+
 # Decode batches (at most this many rows) with an output of at most DECODE_MAX_N
 # columns go to the gfx950 projection kernel; long-K products (K > 4096) only from
 # DECODE_LONG_K_MIN_ROWS rows up. Everything else stays on hipBLASLt through

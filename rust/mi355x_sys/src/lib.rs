@@ -59,6 +59,13 @@ unsafe extern "C" {
         dtype: c_int, stream: *mut c_void) -> *const c_char;
     pub fn mi355x_silu_mul(gate_up: *const c_void, out: *mut c_void, tokens: i64, width: i64,
         dtype: c_int, stream: *mut c_void) -> *const c_char;
+    pub fn mi355x_linear_qk_norm_rope_store(x: *const c_void, ldx: i64, w: *const c_void,
+        ldw: i64, qkv: *mut c_void, ldo: i64, m: i64, k: i64, q_heads: i64, k_heads: i64,
+        workspace: *mut c_void, workspace_bytes: i64, cus: i32, q_weight: *const c_void,
+        k_weight: *const c_void, positions: *const i64, cos: *const f32, sin: *const f32,
+        max_positions: i64, k_cache: *mut c_void, v_cache: *mut c_void, loc: *const c_void,
+        index64: bool, capacity: i64, reserved: i64, error_count: *mut i32, eps: f64,
+        dtype: c_int, stream: *mut c_void) -> *const c_char;
     pub fn mi355x_linear(x: *const c_void, ldx: i64, w: *const c_void, ldw: i64,
         out: *mut c_void, ldo: i64, m: i64, n: i64, k: i64, workspace: *mut c_void,
         workspace_bytes: i64, cus: i32, config: i32, splits: i32, dtype: i64,

@@ -123,6 +123,47 @@ def test_fused_pass_equals_separate_launches(gpu, dtype, index_dtype, stages):
     a2.check_write_errors()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("tokens,hq,hkv,hidden", [(1, 32, 8, 4096), (64, 32, 8, 4096),
+                                                  (256, 32, 8, 4096), (37, 16, 8, 1024),
+                                                  (200, 16, 2, 2048)])
+def test_fused_qkv_projection_pass_equals_the_two_steps(gpu, dtype, tokens, hq, hkv, hidden):
+    """The QKV projection + QK-norm/RoPE/store entry (split-K partials summed inside the pass)
+    against the library's projection followed by the fused pass: packed qkv (q and k rotated,
+    v as projected) and both caches bit for bit, with and without a K split."""
+    from llm_infer_rust_amd import _native
+    from llm_infer_rust_amd._native import lib
+
+    n = (hq + 2 * hkv) * 128
+    g = torch.Generator().manual_seed(tokens + hidden)
+    x = torch.randn(tokens, hidden, generator=g).to(dtype).to(gpu)
+    w = (torch.randn(n, hidden, generator=g) * 0.02).to(dtype).to(gpu)
+    qw = torch.empty(128).uniform_(0.5, 1.5, generator=g).to(dtype).to(gpu)
+    kw = torch.empty(128).uniform_(0.5, 1.5, generator=g).to(dtype).to(gpu)
+    pos = torch.randint(0, 4096, (tokens,), generator=g).to(gpu)
+    rope = ops.HalfSplitRope(4096, 128, 1_000_000.0, gpu)
+    loc = torch.randperm(512 * 16, generator=g)[:tokens]
+    loc[tokens // 2] = 0  # the reserved slot is skipped
+    loc = loc.to(gpu)
+    splits_bytes = lib().mi355x_linear_workspace_bytes(tokens, n, hidden,
+                                                       _native.device_cus(x.device), -1, -1)
+    print(f"tokens {tokens} N {n} K {hidden}: split-K workspace {splits_bytes} bytes")
+
+    a1 = bound_attention(512, 16, hkv, dtype, gpu, 0)
+    qkv1 = ops.decode_linear(x, w)
+    ops.qk_norm_rope_store(qkv1[:, :hq * 128].view(tokens, hq, 128),
+                           qkv1[:, hq * 128:(hq + hkv) * 128].view(tokens, hkv, 128),
+                           qkv1[:, (hq + hkv) * 128:].view(tokens, hkv, 128), qw, kw, 1e-6,
+                           pos, rope, a1, loc)
+    a2 = bound_attention(512, 16, hkv, dtype, gpu, 0)
+    qkv2 = ops.linear_qk_norm_rope_store(x, w, hq, hkv, qw, kw, 1e-6, pos, rope, a2, loc)
+    assert torch.equal(qkv2, qkv1)
+    assert torch.equal(a2.k_cache, a1.k_cache) and torch.equal(a2.v_cache, a1.v_cache)
+    a2.check_write_errors()
+    if (tokens, hidden) == (256, 4096):
+        assert splits_bytes > 0  # the partials route is the one exercised here
+
+
 def test_fused_pass_reports_out_of_range_slot(gpu):
     _, q, k, v = packed_qkv(4, 16, 8, torch.bfloat16, gpu, 5)
     att = bound_attention(8, 1, 8, torch.bfloat16, gpu, -1)
