@@ -613,8 +613,11 @@ def serving_ops_section(dev, reps: int, cpu: bool = True) -> dict:
     joint top-k / top-p sampling of 256 rows x 151,936 (sampling.rs:239-321),
     the fused QK-norm -> RoPE -> K/V store pass of a 256-row decode step and of an 8192-token
     prompt batch, SiLU x mul of the prompt batch, and the four decode-batch projections at 256
-    rows (row f3; fused_ops.cu:108-171,340-372, linear.rs). The projections rotate over two
-    weight sets (~770 MB) so the weights stream from HBM, as in serving."""
+    rows (row f3; fused_ops.cu:108-171,340-372, linear.rs), plus the decode layer's fused QKV
+    projection + QK-norm/RoPE/store route. Kernel figures are device time from a replayed
+    hipGraph of captured calls (``eager_us``: the eager per-call rate beside them); the
+    projections rotate over three weight sets (~1.16 GB) so the weights stream from HBM, as in
+    serving."""
     import numpy as np
     from llm_infer_rust_amd import ops
     from llm_infer_rust_amd.kv_cache import BaseAttention
@@ -636,7 +639,8 @@ def serving_ops_section(dev, reps: int, cpu: bool = True) -> dict:
     nbytes = rows * vocab * 2
     res = {"us": round(ms * 1e3, 2), "rows/s": round(rows / (ms * 1e-3), 1), "bytes": nbytes,
            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
-           "note": "one pass over the logits; the kernel makes up to five (the row stays in L2)"}
+           "note": "eager calls through Sampler (host parameter handling included); bytes are "
+                   "one pass over the logits, the kernel makes up to five (the row stays in L2)"}
     if cpu:
         from oracle import sampling as osamp  # the CPU baseline only
         sample = logits[:8].float().cpu().numpy()
@@ -666,11 +670,14 @@ def serving_ops_section(dev, reps: int, cpu: bool = True) -> dict:
         v = qkv[:, 5120:].view(t, 8, 128)
         positions = torch.randint(0, 2048, (t,), generator=gd, device=dev)
         loc = torch.randperm(pages * 16 - 1, generator=gd, device=dev)[:t] + 1
-        ms = _event_time_ms(lambda: ops.qk_norm_rope_store(q, k, v, qw, kw, 1e-6, positions,
-                                                           rope, att, loc), reps)
+        call = (lambda q=q, k=k, v=v, positions=positions, loc=loc: ops.qk_norm_rope_store(
+            q, k, v, qw, kw, 1e-6, positions, rope, att, loc))
+        eager_ms = _event_time_ms(call, reps)
+        us = _graph_time_us(call)
         nbytes = t * 128 * 2 * (32 * 2 + 8 * 2 + 8 + 16) + 16 * t
-        res = {"us": round(ms * 1e3, 2), "bytes": nbytes,
-               "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        res = {"us": round(us, 2), "bytes": nbytes, "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+               "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+               "eager_us": round(eager_ms * 1e3, 2)}
         if cpu:
             from oracle import layer_ops as olo, norms as onorms  # the CPU baseline only
             n = min(t, 1024)
@@ -700,10 +707,12 @@ def serving_ops_section(dev, reps: int, cpu: bool = True) -> dict:
     # SiLU x mul of the prompt batch: gate_up [8192, 2 x 12288].
     gu = rnd(8192, 2 * 12288)
     act = torch.empty(8192, 12288, dtype=torch.bfloat16, device=dev)
-    ms = _event_time_ms(lambda: ops.silu_and_mul(gu, out=act), reps)
+    eager_ms = _event_time_ms(lambda: ops.silu_and_mul(gu, out=act), reps)
+    us = _graph_time_us(lambda: ops.silu_and_mul(gu, out=act))
     nbytes = 3 * 8192 * 12288 * 2
-    res = {"us": round(ms * 1e3, 2), "bytes": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
-           "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    res = {"us": round(us, 2), "bytes": nbytes, "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+           "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+           "eager_us": round(eager_ms * 1e3, 2)}
     if cpu:
         from oracle import layer_ops as olo  # the CPU baseline only
         sample = gu[:256].float().cpu().numpy()
@@ -719,36 +728,48 @@ def serving_ops_section(dev, reps: int, cpu: bool = True) -> dict:
     x = rnd(256, 12288, scale=0.5)
     shapes = (("qkv", 6144, 4096), ("o_proj", 4096, 4096), ("gate_up_silu", 24576, 4096),
               ("down", 4096, 12288))
-    sets = [{nm: rnd(n, kk, scale=0.02) for nm, n, kk in shapes} for _ in range(2)]
-    for nm, n, kk in shapes:
+    n_sets = 3  # 3 x 386 MB of weights: more than the 256 MB MALL, so they stream from HBM
+    sets = [{nm: rnd(n, kk, scale=0.02) for nm, n, kk in shapes} for _ in range(n_sets)]
+    kc = torch.zeros(2048, 16, 8, 128, dtype=torch.bfloat16, device=dev)
+    att = BaseAttention()
+    att.set_reserved_write_slot(0)
+    att.bind_kv_cache(kc, torch.zeros_like(kc))
+    positions = torch.randint(0, 2048, (256,), generator=gd, device=dev)
+    loc = torch.randperm(2048 * 16 - 1, generator=gd, device=dev)[:256] + 1
+    for nm, n, kk in shapes + (("qkv_norm_rope_store", 6144, 4096),):
         xs = x[:, :kk]
         if nm == "gate_up_silu":
             o = torch.empty(256, n // 2, dtype=torch.bfloat16, device=dev)
-            fn = lambda i, xs=xs, o=o, nm=nm: ops.decode_linear_silu_mul(xs, sets[i % 2][nm], out=o)
+            fn = lambda i, xs=xs, o=o, nm=nm: ops.decode_linear_silu_mul(
+                xs, sets[i % n_sets][nm], out=o)
+        elif nm == "qkv_norm_rope_store":  # the decode layer's fused QKV route
+            fn = lambda i, xs=xs: ops.linear_qk_norm_rope_store(
+                xs, sets[i % n_sets]["qkv"], 32, 8, qw, kw, 1e-6, positions, rope, att, loc)
         else:
             o = torch.empty(256, n, dtype=torch.bfloat16, device=dev)
-            fn = lambda i, xs=xs, o=o, nm=nm: ops.decode_linear(xs, sets[i % 2][nm], out=o)
+            fn = lambda i, xs=xs, o=o, nm=nm: ops.decode_linear(xs, sets[i % n_sets][nm], out=o)
         state = {"i": 0}
 
         def step(fn=fn, state=state):
             fn(state["i"])
             state["i"] += 1
-        ms = _event_time_ms(step, reps)
+        eager_ms = _event_time_ms(step, reps)
+        us = _graph_time_us(step, launches=3 * n_sets * 10)  # the captured calls rotate the sets
         wbytes = n * kk * 2
         flops = 2 * 256 * n * kk
-        res = {"us": round(ms * 1e3, 2), "weight_bytes": wbytes,
-               "TB/s": round(wbytes / (ms * 1e-3) / 1e12, 3),
-               "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}
+        res = {"us": round(us, 2), "weight_bytes": wbytes,
+               "TB/s": round(wbytes / (us * 1e-6) / 1e12, 3),
+               "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1), "eager_us": round(eager_ms * 1e3, 2)}
         if cpu:
             xc = xs[:16].float().cpu()
-            wc = sets[0][nm].float().cpu()
+            wc = sets[0]["qkv" if nm == "qkv_norm_rope_store" else nm].float().cpu()
             cms, threads = _cpu_median_ms(lambda: xc @ wc.T)
             res["cpu_baseline"] = {"value": round(2 * 16 * n * kk / (cms * 1e-3) / 1e9, 2),
                                    "unit": "GFLOP/s", "cores": threads, "kind": "port",
                                    "sample": "16 of the 256 rows, torch-CPU fp32 x @ w^T "
                                              "(linear.rs:5-7), median of 3"}
         out[f"linear_256_{nm}"] = res
-    del sets, x
+    del sets, x, kc, att
     torch.cuda.empty_cache()
     return out
 
