@@ -223,9 +223,11 @@ def linear_qk_norm_rope_store(x: torch.Tensor, weight: torch.Tensor, q_heads: in
     runs the two steps."""
     m, k = (x.shape if x.dim() == 2 else (0, 0))
     n = weight.size(0)
-    d = 128
+    if q_heads <= 0 or k_heads <= 0 or n % (q_heads + 2 * k_heads):
+        raise NativeError("QKV weight rows must be (q_heads + 2 k_heads) * head_dim")
+    d = n // (q_heads + 2 * k_heads)  # head_dim
     fused = (x.is_cuda and x.dim() == 2 and x.stride(1) == 1 and x.stride(0) % 8 == 0
-             and weight.is_contiguous() and n == (q_heads + 2 * k_heads) * d
+             and weight.is_contiguous() and d == 128
              and uses_decode_kernel(m, n, k) and attention is not None
              and write_loc is not None and attention.is_bound() and rope_tables is not None)
     if not fused:
