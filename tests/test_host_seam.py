@@ -79,3 +79,20 @@ def test_kv_pool_layout():
     assert KVCacheLayout(28, 100, 16, 8, 128).tensor_shape() == (2, 28, 101, 16, 8, 128)
     with pytest.raises(ModelError):
         KVCacheLayout(28, 0, 16, 8, 128).tensor_shape()
+
+
+def test_fused_qkv_route_checks_the_weight_shape():
+    """``ops.linear_qk_norm_rope_store`` derives head_dim from the QKV weight: rows that are not
+    a whole number of (Hq + 2 Hkv) heads are refused before anything runs."""
+    import torch
+
+    from llm_infer_rust_amd import ops
+    from llm_infer_rust_amd._native import NativeError
+
+    x = torch.zeros(4, 64)
+    with pytest.raises(NativeError, match="q_heads \\+ 2 k_heads"):
+        ops.linear_qk_norm_rope_store(x, torch.zeros(3 * 128 + 1, 64), 1, 1, None, None, 1e-6,
+                                      None, None, None, None)
+    with pytest.raises(NativeError, match="q_heads \\+ 2 k_heads"):
+        ops.linear_qk_norm_rope_store(x, torch.zeros(512, 64), 0, 2, None, None, 1e-6, None,
+                                      None, None, None)
