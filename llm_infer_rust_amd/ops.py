@@ -249,7 +249,8 @@ def linear_qk_norm_rope_store(x: torch.Tensor, weight: torch.Tensor, q_heads: in
     cos, sin, max_pos = rope_tables.cos, rope_tables.sin, rope_tables.max_positions
     _check_positions(q_view, positions, cos, sin)
     kc, vc = attention.cache_tensors()
-    if kc.size(2) != k_heads or kc.size(3) != d or kc.dtype != x.dtype:
+    if (kc.size(2) != k_heads or kc.size(3) != d or kc.dtype != x.dtype
+            or kc.device != x.device):
         raise NativeError("K/V input head shape does not match the bound cache")
     if (write_loc.dim() != 1 or write_loc.numel() != m or not write_loc.is_contiguous()
             or write_loc.dtype not in (torch.int32, torch.int64) or write_loc.device != x.device):
