@@ -562,6 +562,22 @@ def ceilings_section(dev, w, reps: int) -> dict:
             ms = timed(g, reps)
             sweep[f"{label}_d{depth}_wg{blocks}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
     out["gather_sweep_GB/s"] = sweep
+    # Per-CU rate of direct global -> LDS copies (8 waves x 8 KiB in flight per workgroup),
+    # all from HBM and half from L2, at the QKV projection's 192 workgroups and at 256.
+    lib.mi355x_calib_load_rate.restype = ctypes.c_char_p
+    lib.mi355x_calib_load_rate.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                                           ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
+    span = 6 << 30  # inside one 8 GiB pool: a multiple of 192 and 256 x 8 MiB
+    load = {}
+    for blocks in (192, 256):
+        iters = span // (blocks * 8 * 1024 * 8) // 2  # each wave walks half its region
+        for mix in (0, 1):
+            ms = timed(lambda i, b=blocks, m=mix, it=iters: check(lib.mi355x_calib_load_rate(
+                ctypes.c_void_p(w["kcs"][i % LAYERS].data_ptr()), span, it, m, b, stream)), reps)
+            moved = blocks * 8 * iters * 8 * 1024
+            load[f"{'mixed_l2_hbm' if mix else 'hbm'}_wg{blocks}"] = round(
+                moved / (ms * 1e-3) / 1e9 / blocks, 1)
+    out["load_rate_GB/s_per_CU"] = load
     ms = timed(stream_read, reps)
     out["stream_read"] = {"us": round(ms * 1e3, 2), "bytes": nbytes,
                           "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}

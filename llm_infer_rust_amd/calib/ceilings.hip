@@ -359,6 +359,52 @@ extern "C" __attribute__((visibility("default"))) const char* mi355x_calib_gathe
   return hipGetLastError() == hipSuccess ? nullptr : "gather launch failed";
 }
 
+// Per-CU load rate of direct global -> LDS copies (the copy the projection and decode kernels
+// use): 8 waves per workgroup, each keeping 8 KiB in flight (eight 1 KiB copies per trip, wait
+// until 8 remain) on a stream of its own through `bytes` of memory (a multiple of
+// blocks * 8 * 1 MiB). With MIX every other copy reads a 1 MiB block at the end of the buffer,
+// which stays in L2, so a CU's load queue carries half L2 hits and half HBM misses.
+typedef __attribute__((address_space(3))) uint8_t calib_lds_u8;
+
+template <bool MIX>
+__global__ __launch_bounds__(512, 1) void load_rate(const uint8_t* __restrict__ buf, int64_t bytes,
+                                                    int iters) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[65536];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (iters < 0) lds[threadIdx.x] = 0;  // never taken; the copies' LDS writes are invisible
+  const uint32_t base =
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const calib_lds_u8*)lds)) + wave * 8192;
+  const int64_t region = bytes / (int64_t(gridDim.x) * 8);
+  const int64_t off = (int64_t(blockIdx.x) * 8 + wave) * region;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const int64_t k = (int64_t(it) * 8 + d) * 1024;
+      const uint8_t* p = (MIX && (d & 1))
+                             ? buf + bytes - (1 << 20) + ((k + wave * 65536) & ((1 << 20) - 1))
+                             : buf + off + k % region;
+      asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(base + d * 1024),
+                   "v"(p + lane * 16)
+                   : "m0");
+    }
+    __builtin_amdgcn_s_waitcnt((8 & 15) | (7 << 4) | (15 << 8));  // vmcnt(8)
+  }
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+}
+
+extern "C" __attribute__((visibility("default"))) const char* mi355x_calib_load_rate(
+    const void* buf, int64_t bytes, int32_t iters, int32_t mix, int32_t blocks, void* stream) {
+  if (blocks <= 0 || iters <= 0 || bytes % (int64_t(blocks) * 8 * (1 << 20)))
+    return "load rate: bytes must be a multiple of blocks * 8 MiB";
+  auto s = static_cast<hipStream_t>(stream);
+  auto b = static_cast<const uint8_t*>(buf);
+  if (mix)
+    load_rate<true><<<blocks, 512, 0, s>>>(b, bytes, iters);
+  else
+    load_rate<false><<<blocks, 512, 0, s>>>(b, bytes, iters);
+  return hipGetLastError() == hipSuccess ? nullptr : "load rate launch failed";
+}
+
 // The same gather with DEPTH rows in flight per wave (1, 2, 4 or 8) over `blocks`
 // workgroups: the in-flight sweep that shows where the pattern saturates.
 extern "C" __attribute__((visibility("default"))) const char* mi355x_calib_gather_depth(
