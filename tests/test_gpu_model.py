@@ -243,3 +243,36 @@ def test_decode_staged_ahead_matches_unstaged(gpu):
     assert cut[0] == plain[0][:stop + 1]
     assert cut[1:] == plain[1:]
     assert st_eos["ahead_steps"] > 0
+
+
+def test_staged_decode_step_is_discarded_when_a_request_arrives(gpu):
+    """A request added between steps while every running request decodes: the next step runs
+    its prefill first (which rewrites the pinned staging block) and must not use the decode step
+    staged before. Greedy tokens must equal a run with staging off, step for step."""
+    model, _ = build(TINY, 14, gpu)
+    rng = np.random.default_rng(15)
+    first = [rng.integers(0, TINY.vocab_size, n) for n in (12, 25)]
+    late = rng.integers(0, TINY.vocab_size, 19)
+
+    def run(staged):
+        eng = Engine(model, EngineConfig(max_running_req=4, max_seq_len=128, seed=5,
+                                         graph_batch_sizes=(4,)))
+        if not staged:
+            eng._prepare_ahead = lambda rows: None
+        reqs = [eng.add_request(p, SamplingParams(max_tokens=9)) for p in first]
+        for _ in range(4):  # one prefill step, then decode steps that stage their successors
+            eng.step()
+        if staged:
+            assert eng._ahead is not None  # a step is staged when the request arrives
+        reqs.append(eng.add_request(late, SamplingParams(max_tokens=9)))
+        eng.run_until_complete()
+        out = [list(r.output) for r in reqs]
+        stats = dict(eng.stats)
+        del eng
+        torch.cuda.synchronize()
+        return out, stats
+
+    plain, _ = run(False)
+    staged, stats = run(True)
+    assert staged == plain and all(len(o) == 9 for o in staged)
+    assert stats["ahead_steps"] > 0
