@@ -456,9 +456,13 @@ class Engine:
 
     # ------------------------------------------------------------------ loop
     def step(self) -> None:
+        """Prefill, then decode every running request (``scheduler.rs:204-271`` step_serial);
+        a step whose prefill ran a chunk that is not its request's last ends there."""
         picked = self._select_prefill()
         if picked:
             self._run_prefill(picked)
+            if any(req.cursor < req.prompt.size for req, _ in picked):
+                return
         rows = self._decode_rows()
         if rows:
             self._run_decode(rows)

@@ -276,3 +276,25 @@ def test_staged_decode_step_is_discarded_when_a_request_arrives(gpu):
     staged, stats = run(True)
     assert staged == plain and all(len(o) == 9 for o in staged)
     assert stats["ahead_steps"] > 0
+
+
+def test_non_final_prefill_chunk_ends_the_step(gpu):
+    """``scheduler.rs`` step_serial: a step whose prefill batch carries a chunk that is not its
+    request's last returns before decode. A short request admitted with a long one therefore
+    holds its first token until the long prompt's last chunk has run."""
+    model, _ = build(TINY, 16, gpu)
+    rng = np.random.default_rng(17)
+    eng = Engine(model, EngineConfig(page_size=16, max_running_req=2,
+                                     max_prefill_tokens_per_batch=48, max_seq_len=256,
+                                     use_graphs=False))
+    short = eng.add_request(rng.integers(0, TINY.vocab_size, 8), SamplingParams(max_tokens=4))
+    long = eng.add_request(rng.integers(0, TINY.vocab_size, 120), SamplingParams(max_tokens=4))
+    eng.step()  # short (8) + the long prompt's first chunk (32, page-aligned): no decode
+    assert len(short.output) == 1 and long.cursor == 32 and eng.stats["decode_steps"] == 0
+    while long.cursor < long.prompt.size:
+        eng.step()
+        if long.cursor < long.prompt.size:
+            assert eng.stats["decode_steps"] == 0 and len(short.output) == 1
+    assert eng.stats["decode_steps"] == 1 and len(short.output) == 2  # the last chunk's step
+    eng.run_until_complete()
+    assert len(short.output) == 4 and len(long.output) == 4
