@@ -3,24 +3,25 @@
 //!
 //! Drop-in for the reference server: this file becomes `src/models/attention/mi355x.rs`, a
 //! child module of `backend.rs` (so it sees the private `AttentionBackend` trait,
-//! `backend.rs:262-306`), declared there with `#[cfg(has_mi355x)] mod mi355x;`. It follows
-//! `FlashInferAttentionBackend` (`backend.rs:316-804`) step for step: one decode plan and one
-//! prefill plan per backend, re-planned once per forward and reused by every layer; graph
-//! plans registered under the block-table address and re-planned outside capture; the same
-//! error strings. The only differences are the ABI (raw pointers, strides and the ATen
-//! current stream instead of `at::Tensor*`) and that no output tensor is allocated by the
-//! library: decode and prefill write into a tensor allocated here (or the caller's static
-//! output in `forward_into`).
+//! `backend.rs:262-306`), declared there with `#[cfg(has_mi355x)] mod mi355x;`. It keeps the
+//! trait's contract (one plan per forward, reused by every layer; graph plans re-made
+//! outside capture at a fixed address; the decode/prefill routing of `forward`) and the
+//! reference's error strings, so callers see the same behaviour.
 //!
-//! The edits to `backend.rs` that wire it in are listed in the repository's integration
-//! guide (new `AttentionBackendKind::Mi355x`, its `parse` names, `validate`,
-//! `create_attention_backend`, two `BackendPlan` variants and the `forward_into` arm).
+//! Plan lifetime is this module's own: every native plan lives in a `PlanOwner`, which
+//! knows which `*_plan_drop` entry frees it and carries two flags. `leased` is set while a
+//! batch holds the backend's decode or prefill plan (a `Mi355xLease`; re-planning it then
+//! fails, since the batch's layers still read it). `retired` is set when the decode graph
+//! that registered a graph plan is dropped; retired graph plans leave the registry at the
+//! next lookup, and the native plan is freed when its last holder lets go.
+//!
+//! No output tensor is allocated by the library: decode and prefill write into a tensor
+//! allocated here (or the caller's static output in `forward_into`).
 
 use std::{
-    cell::RefCell,
-    collections::HashMap,
+    cell::{Cell, RefCell},
     ffi::c_void,
-    rc::{Rc, Weak},
+    rc::Rc,
 };
 
 use mi355x_sys as sys;
@@ -35,32 +36,145 @@ use super::{
     PrefillMetadata, Result, model_error,
 };
 
-/// An opaque native plan and the entry that frees it.
-pub(super) struct Mi355xPlan {
-    handle: *mut c_void,
-    prefill: bool,
-    /// The KV cache page size the plan was made for (the run entries check it).
-    page_size: i64,
+/// Which native planner made a plan; selects the entry that frees it.
+#[derive(Clone, Copy, PartialEq, Eq)]
+enum PlanKind {
+    Decode,
+    Prefill,
 }
 
-impl Drop for Mi355xPlan {
+/// One native plan handle (null until the first prepare) and its lease state.
+pub(super) struct PlanOwner {
+    kind: PlanKind,
+    handle: Cell<*mut c_void>,
+    /// KV page size of the last prepare (the run entries check it against the plan).
+    page_size: Cell<i64>,
+    /// A batch holds this plan; it must not be re-planned until the batch is dropped.
+    leased: Cell<bool>,
+    /// Graph plans only: the graph that registered it is gone.
+    retired: Cell<bool>,
+}
+
+impl PlanOwner {
+    fn new(kind: PlanKind) -> Rc<Self> {
+        Rc::new(Self {
+            kind,
+            handle: Cell::new(std::ptr::null_mut()),
+            page_size: Cell::new(0),
+            leased: Cell::new(false),
+            retired: Cell::new(false),
+        })
+    }
+
+    /// Runs a native prepare on this owner's handle (null makes a new plan) and keeps the
+    /// handle it returns. The native planners re-plan an existing handle in place.
+    fn replan(
+        &self,
+        page_size: i64,
+        prepare: impl FnOnce(*mut c_void) -> Result<*mut c_void>,
+    ) -> Result<()> {
+        let before = self.handle.get();
+        let after = prepare(before)?;
+        if !before.is_null() && after != before {
+            return Err(model_error("graph plan address changed"));
+        }
+        self.handle.set(after);
+        self.page_size.set(page_size);
+        Ok(())
+    }
+}
+
+impl Drop for PlanOwner {
     fn drop(&mut self) {
+        let handle = self.handle.get();
+        if handle.is_null() {
+            return;
+        }
         // The library waits for the plan's pending uploads before freeing it.
         unsafe {
-            if self.prefill {
-                sys::mi355x_prefill_plan_drop(self.handle)
-            } else {
-                sys::mi355x_decode_plan_drop(self.handle)
+            match self.kind {
+                PlanKind::Decode => sys::mi355x_decode_plan_drop(handle),
+                PlanKind::Prefill => sys::mi355x_prefill_plan_drop(handle),
             }
         }
     }
 }
 
+/// A batch's hold on a plan, carried in `BackendPlan::Mi355x{Decode,Prefill}`. An
+/// exclusive lease (the backend's per-forward plans) clears `leased` when dropped; a graph
+/// plan is shared by every replay and is never leased exclusively.
+pub(super) struct Mi355xLease {
+    owner: Rc<PlanOwner>,
+    exclusive: bool,
+}
+
+impl Mi355xLease {
+    fn exclusive(owner: &Rc<PlanOwner>, busy: &str) -> Result<Self> {
+        if owner.leased.replace(true) {
+            return Err(model_error(busy));
+        }
+        Ok(Self {
+            owner: Rc::clone(owner),
+            exclusive: true,
+        })
+    }
+
+    fn shared(owner: &Rc<PlanOwner>) -> Self {
+        Self {
+            owner: Rc::clone(owner),
+            exclusive: false,
+        }
+    }
+
+    fn handle(&self) -> *mut c_void {
+        self.owner.handle.get()
+    }
+
+    fn page_size(&self) -> i64 {
+        self.owner.page_size.get()
+    }
+}
+
+impl Drop for Mi355xLease {
+    fn drop(&mut self) {
+        if self.exclusive {
+            self.owner.leased.set(false);
+        }
+    }
+}
+
+/// Graph plans of the live decode graphs, found by the address of the block table the
+/// graph was captured on (a handful of batch buckets, so a short list).
 #[derive(Default)]
+struct GraphPlans(Vec<(usize, Rc<PlanOwner>)>);
+
+impl GraphPlans {
+    fn prune(&mut self) {
+        self.0.retain(|(_, owner)| !owner.retired.get());
+    }
+
+    fn find(&self, table_addr: usize) -> Option<&Rc<PlanOwner>> {
+        self.0
+            .iter()
+            .find(|(addr, owner)| *addr == table_addr && !owner.retired.get())
+            .map(|(_, owner)| owner)
+    }
+}
+
 pub(super) struct Mi355xAttentionBackend {
-    plan: RefCell<Option<Rc<Mi355xPlan>>>,
-    prefill_plan: RefCell<Option<Rc<Mi355xPlan>>>,
-    graph_plans: RefCell<HashMap<usize, Weak<Mi355xPlan>>>,
+    decode: Rc<PlanOwner>,
+    prefill: Rc<PlanOwner>,
+    graphs: RefCell<GraphPlans>,
+}
+
+impl Default for Mi355xAttentionBackend {
+    fn default() -> Self {
+        Self {
+            decode: PlanOwner::new(PlanKind::Decode),
+            prefill: PlanOwner::new(PlanKind::Prefill),
+            graphs: RefCell::new(GraphPlans::default()),
+        }
+    }
 }
 
 fn dtype_code(kind: Kind) -> Result<i64> {
@@ -82,6 +196,10 @@ fn check(status: *const std::ffi::c_char, what: &str) -> Result<()> {
     sys::check(status).map_err(|error| model_error(&format!("{what}: {error}")))
 }
 
+fn bound_page_size(page_size: Option<i64>) -> Result<i64> {
+    page_size.ok_or_else(|| model_error("mi355x requires a bound KV cache"))
+}
+
 impl AttentionBackend for Mi355xAttentionBackend {
     fn metadata_requirements(&self, _phase: BatchPhase) -> MetadataRequirements {
         MetadataRequirements {
@@ -100,32 +218,29 @@ impl AttentionBackend for Mi355xAttentionBackend {
         spec: AttentionSpec,
         page_size: i64,
     ) -> Result<Option<Box<dyn DecodeGraphState>>> {
-        let table = metadata
-            .block_table
-            .as_ref()
-            .ok_or_else(|| model_error("missing graph block_table"))?;
-        let lengths = metadata
-            .cache_seqlens
-            .as_ref()
-            .ok_or_else(|| model_error("missing graph cache_seqlens"))?;
-        let plan = Rc::new(Mi355xPlan {
-            handle: prepare_decode(metadata, spec, page_size, std::ptr::null_mut(), true)?,
-            prefill: false,
-            page_size,
-        });
-        let mut plans = self.graph_plans.borrow_mut();
-        plans.retain(|_, plan| plan.strong_count() > 0);
-        let key = table.data_ptr() as usize;
-        if plans.get(&key).and_then(Weak::upgrade).is_some() {
+        let (Some(table), Some(lengths)) = (&metadata.block_table, &metadata.cache_seqlens) else {
+            return Err(model_error(if metadata.block_table.is_none() {
+                "missing graph block_table"
+            } else {
+                "missing graph cache_seqlens"
+            }));
+        };
+        let mut graphs = self.graphs.borrow_mut();
+        graphs.prune();
+        let addr = table.data_ptr() as usize;
+        if graphs.find(addr).is_some() {
             return Err(model_error("decode graph buffers are already registered"));
         }
-        plans.insert(key, Rc::downgrade(&plan));
+        let owner = PlanOwner::new(PlanKind::Decode);
+        owner.replan(page_size, |existing| {
+            prepare_decode(metadata, spec, page_size, existing, true)
+        })?;
+        graphs.0.push((addr, Rc::clone(&owner)));
         Ok(Some(Box::new(Mi355xGraphState {
-            plan,
+            owner,
             table: table.shallow_clone(),
             lengths: lengths.shallow_clone(),
             spec,
-            page_size,
         })))
     }
 
@@ -136,61 +251,35 @@ impl AttentionBackend for Mi355xAttentionBackend {
         spec: AttentionSpec,
         page_size: Option<i64>,
     ) -> Result<BackendPlan> {
-        if let Some(metadata) = metadata.filter(|meta| meta.forward_mode == BatchPhase::Decode) {
-            if let Some(plan) = metadata.block_table.as_ref().and_then(|table| {
-                self.graph_plans
-                    .borrow()
-                    .get(&(table.data_ptr() as usize))
-                    .and_then(Weak::upgrade)
-            }) {
-                // Planned outside capture/replay: no device read-back, no allocation.
-                return Ok(BackendPlan::Mi355xDecode(plan));
+        let Some(metadata) = metadata else {
+            return FlashAttentionBackend.prepare(metadata, prefill, spec, page_size);
+        };
+        if metadata.forward_mode == BatchPhase::Decode {
+            // A replayed graph's plan was re-made outside capture by `prepare_replay`: hand
+            // it out as is (no device read-back, no allocation during capture).
+            if let Some(table) = &metadata.block_table {
+                if let Some(owner) = self.graphs.borrow().find(table.data_ptr() as usize) {
+                    return Ok(BackendPlan::Mi355xDecode(Mi355xLease::shared(owner)));
+                }
             }
-            let page_size =
-                page_size.ok_or_else(|| model_error("mi355x requires a bound KV cache"))?;
-            let mut cached = self.plan.borrow_mut();
-            if cached
-                .as_ref()
-                .is_some_and(|plan| Rc::strong_count(plan) != 1)
-            {
-                return Err(model_error("previous mi355x batch is still in use"));
-            }
-            let existing = cached.as_ref().map_or(std::ptr::null_mut(), |plan| plan.handle);
-            let handle = prepare_decode(metadata, spec, page_size, existing, false)?;
-            let plan = cached.get_or_insert_with(|| {
-                Rc::new(Mi355xPlan {
-                    handle,
-                    prefill: false,
-                    page_size,
-                })
-            });
-            return Ok(BackendPlan::Mi355xDecode(Rc::clone(plan)));
+            let page_size = bound_page_size(page_size)?;
+            let lease =
+                Mi355xLease::exclusive(&self.decode, "previous mi355x batch is still in use")?;
+            // On failure the lease drops here and frees the plan for the next attempt.
+            self.decode.replan(page_size, |existing| {
+                prepare_decode(metadata, spec, page_size, existing, false)
+            })?;
+            return Ok(BackendPlan::Mi355xDecode(lease));
         }
-        if let Some(metadata) = metadata {
-            let mut cached = self.prefill_plan.borrow_mut();
-            if cached
-                .as_ref()
-                .is_some_and(|plan| Rc::strong_count(plan) != 1)
-            {
-                return Err(model_error("previous mi355x prefill batch is still in use"));
-            }
-            let existing = cached.as_ref().map_or(std::ptr::null_mut(), |plan| plan.handle);
-            let page_size =
-                page_size.ok_or_else(|| model_error("mi355x requires a bound KV cache"))?;
-            let handle = prepare_prefill(metadata, prefill, spec, page_size, existing)?;
-            let plan = cached.get_or_insert_with(|| {
-                Rc::new(Mi355xPlan {
-                    handle,
-                    prefill: true,
-                    page_size,
-                })
-            });
-            return Ok(BackendPlan::Mi355xPrefill(
-                Rc::clone(plan),
-                prefill.has_prefix(),
-            ));
-        }
-        FlashAttentionBackend.prepare(metadata, prefill, spec, page_size)
+        let page_size = bound_page_size(page_size)?;
+        let lease = Mi355xLease::exclusive(
+            &self.prefill,
+            "previous mi355x prefill batch is still in use",
+        )?;
+        self.prefill.replan(page_size, |existing| {
+            prepare_prefill(metadata, prefill, spec, page_size, existing)
+        })?;
+        Ok(BackendPlan::Mi355xPrefill(lease, prefill.has_prefix()))
     }
 
     fn forward(
@@ -206,43 +295,50 @@ impl AttentionBackend for Mi355xAttentionBackend {
         head_dim: i64,
         plan: &BackendPlan,
     ) -> Result<Tensor> {
-        if metadata.is_some_and(|meta| meta.forward_mode == BatchPhase::Decode) {
-            return mi355x_decode(q, cache, plan, num_kv_heads, head_dim, None);
+        match metadata.map(|meta| meta.forward_mode) {
+            Some(BatchPhase::Decode) => mi355x_decode(q, cache, plan, num_kv_heads, head_dim, None),
+            Some(_) => mi355x_prefill(q, k, v, cache, plan, num_kv_heads, head_dim, None),
+            None => FlashAttentionBackend.forward(
+                q,
+                k,
+                v,
+                cache,
+                prefill,
+                metadata,
+                num_heads,
+                num_kv_heads,
+                head_dim,
+                plan,
+            ),
         }
-        if metadata.is_some() {
-            return mi355x_prefill(q, k, v, cache, plan, num_kv_heads, head_dim, None);
-        }
-        FlashAttentionBackend.forward(
-            q,
-            k,
-            v,
-            cache,
-            prefill,
-            metadata,
-            num_heads,
-            num_kv_heads,
-            head_dim,
-            plan,
-        )
     }
 }
 
-/// Graph-mode decode plan: fixed rows and columns, re-planned at a fixed address before
-/// every replay (`FlashInferGraphState`, `backend.rs:490-530`).
+/// Decode graph state: the graph's own plan, sized for the captured bucket, re-made in
+/// place before every replay. Dropping it retires the plan from the backend's registry.
 struct Mi355xGraphState {
-    plan: Rc<Mi355xPlan>,
+    owner: Rc<PlanOwner>,
     table: Tensor,
     lengths: Tensor,
     spec: AttentionSpec,
-    page_size: i64,
+}
+
+impl Drop for Mi355xGraphState {
+    fn drop(&mut self) {
+        self.owner.retired.set(true);
+    }
 }
 
 impl DecodeGraphState for Mi355xGraphState {
     fn prepare_replay(&self, host: Option<&DecodeHostMetadata>) -> Result<()> {
-        // Pad rows of the captured bucket read page 0 with length 1 and write slot 0.
-        let host = host.map(|host| {
-            let mut cache_seqlens = host.cache_seqlens.clone();
-            cache_seqlens.resize(self.table.size()[0] as usize, 1);
+        // The captured bucket has `rows` rows; rows past the live batch are pad rows that
+        // read page 0 with length 1 (and write the reserved slot), so their host length is 1.
+        let rows = self.table.size()[0] as usize;
+        let decode_host = host.map(|host| {
+            let live = host.cache_seqlens.len().min(rows);
+            let mut cache_seqlens = Vec::with_capacity(rows);
+            cache_seqlens.extend_from_slice(&host.cache_seqlens[..live]);
+            cache_seqlens.extend(std::iter::repeat(1).take(rows - live));
             DecodeHostMetadata {
                 cache_seqlens,
                 block_table_versions: None,
@@ -250,7 +346,7 @@ impl DecodeGraphState for Mi355xGraphState {
         });
         let metadata = AttentionMetadata {
             forward_mode: BatchPhase::Decode,
-            decode_host: host,
+            decode_host,
             write_loc: None,
             cu_seqlens_q: None,
             prefix_lens: None,
@@ -259,11 +355,11 @@ impl DecodeGraphState for Mi355xGraphState {
             req_to_token: None,
             max_seqlen: None,
         };
-        let handle = prepare_decode(&metadata, self.spec, self.page_size, self.plan.handle, true)?;
-        if handle != self.plan.handle {
-            return Err(model_error("graph plan address changed"));
-        }
-        Ok(())
+        let page_size = self.owner.page_size.get();
+        // `replan` refuses a handle that moved: the captured kernels hold its address.
+        self.owner.replan(page_size, |existing| {
+            prepare_decode(&metadata, self.spec, page_size, existing, true)
+        })
     }
 
     fn needs_req_to_token(&self) -> bool {
@@ -292,7 +388,10 @@ fn prepare_decode(
         return Err(model_error("invalid decode block table or lengths"));
     }
     let (rows, cols) = (table.size()[0], table.size()[1]);
-    let host = metadata.decode_host.as_ref();
+    let (host_ptr, host_rows) = match &metadata.decode_host {
+        Some(host) => (host.cache_seqlens.as_ptr(), host.cache_seqlens.len() as i64),
+        None => (std::ptr::null(), 0),
+    };
     let prepared = unsafe {
         sys::mi355x_decode_prepare(
             existing,
@@ -307,8 +406,8 @@ fn prepare_decode(
             page_size,
             dtype_code(spec.kind)?,
             graph,
-            host.map_or(std::ptr::null(), |host| host.cache_seqlens.as_ptr()),
-            host.map_or(0, |host| host.cache_seqlens.len() as i64),
+            host_ptr,
+            host_rows,
             stream_of(spec.device),
         )
     };
@@ -340,15 +439,18 @@ fn prepare_prefill(
     }
     let boundaries: Vec<i32> = prefill.boundaries.iter().map(|&v| v as i32).collect();
     let prefixes: Vec<i32> = prefill.prefixes.iter().map(|&v| v as i32).collect();
-    let batch = prefixes.len() as i64;
+    let (table_ptr, columns, stride) = match table {
+        Some(t) => (t.data_ptr().cast_const().cast(), t.size()[1], t.stride()[0]),
+        None => (std::ptr::null(), 0, 0),
+    };
     let prepared = unsafe {
         sys::mi355x_prefill_prepare(
             existing,
             cumulative.data_ptr().cast(),
-            table.map_or(std::ptr::null(), |t| t.data_ptr().cast()),
-            batch,
-            table.map_or(0, |t| t.size()[1]),
-            table.map_or(0, |t| t.stride()[0]),
+            table_ptr,
+            prefixes.len() as i64,
+            columns,
+            stride,
             boundaries.as_ptr(),
             prefixes.as_ptr(),
             spec.num_heads,
@@ -367,6 +469,14 @@ fn prepare_prefill(
     Ok(prepared)
 }
 
+/// The output a run writes: the caller's static tensor, or a new [tokens, heads * 128].
+fn output_for(q: &Tensor, head_dim: i64, output: Option<&Tensor>) -> Tensor {
+    match output {
+        Some(out) => out.shallow_clone(),
+        None => Tensor::empty([q.size()[0], q.size()[1] * head_dim], (q.kind(), q.device())),
+    }
+}
+
 /// Paged decode into `output` ([tokens, heads * 128], contiguous) or a new tensor. The
 /// query may be a strided view of packed QKV (no contiguous copy, unlike
 /// `backend.rs:651`).
@@ -381,20 +491,17 @@ pub(super) fn mi355x_decode(
     if !matches!(q.device(), Device::Cuda(_)) {
         return Err(model_error("mi355x decode requires a GPU device"));
     }
-    let BackendPlan::Mi355xDecode(plan) = plan else {
+    let BackendPlan::Mi355xDecode(lease) = plan else {
         return Err(model_error("mi355x decode requires a prepared batch"));
     };
     let (k_cache, v_cache) = cache.cache_tensors()?;
+    let out = output_for(q, head_dim, output);
     let (tokens, heads) = (q.size()[0], q.size()[1]);
-    let out = output.map_or_else(
-        || Tensor::empty([tokens, heads * head_dim], (q.kind(), q.device())),
-        Tensor::shallow_clone,
-    );
     let qs = q.stride();
     check(
         unsafe {
             sys::mi355x_decode_run(
-                plan.handle,
+                lease.handle(),
                 q.data_ptr().cast_const(),
                 qs[0],
                 qs[1],
@@ -406,7 +513,7 @@ pub(super) fn mi355x_decode(
                 tokens,
                 heads,
                 num_kv_heads,
-                plan.page_size,
+                lease.page_size(),
                 dtype_code(q.kind())?,
                 stream_of(q.device()),
             )
@@ -427,47 +534,44 @@ pub(super) fn mi355x_prefill(
     head_dim: i64,
     output: Option<&Tensor>,
 ) -> Result<Tensor> {
-    let BackendPlan::Mi355xPrefill(plan, paged) = plan else {
+    let BackendPlan::Mi355xPrefill(lease, paged) = plan else {
         return Err(model_error("missing mi355x prefill plan"));
     };
-    // Paged plans read the layer's whole cache [pages, page, kv_heads, 128]; ragged plans
-    // read the (packed) K/V projection rows in place.
-    let cached;
-    let (k, v, k_sn, k_sh, v_sn, v_sh) = if *paged {
-        cached = cache.cache_tensors()?;
-        let (kc, vc) = cached;
+    // Paged plans read the layer's whole cache [pages, page, kv_heads, 128] (row stride
+    // kv_heads * 128, head stride 128); ragged plans read the (packed) K/V projection rows
+    // in place with their own strides.
+    let layer_cache;
+    let (k_src, v_src, k_strides, v_strides) = if *paged {
+        layer_cache = cache.cache_tensors()?;
         let row = num_kv_heads * head_dim;
-        (kc, vc, row, head_dim, row, head_dim)
+        (&layer_cache.0, &layer_cache.1, [row, head_dim], [row, head_dim])
     } else {
         let (ks, vs) = (k.stride(), v.stride());
-        (k, v, ks[0], ks[1], vs[0], vs[1])
+        (k, v, [ks[0], ks[1]], [vs[0], vs[1]])
     };
+    let out = output_for(q, head_dim, output);
     let (tokens, heads) = (q.size()[0], q.size()[1]);
-    let out = output.map_or_else(
-        || Tensor::empty([tokens, heads * head_dim], (q.kind(), q.device())),
-        Tensor::shallow_clone,
-    );
     let qs = q.stride();
     check(
         unsafe {
             sys::mi355x_prefill_run(
-                plan.handle,
+                lease.handle(),
                 q.data_ptr().cast_const(),
                 qs[0],
                 qs[1],
-                k.data_ptr().cast_const(),
-                k_sn,
-                k_sh,
-                v.data_ptr().cast_const(),
-                v_sn,
-                v_sh,
+                k_src.data_ptr().cast_const(),
+                k_strides[0],
+                k_strides[1],
+                v_src.data_ptr().cast_const(),
+                v_strides[0],
+                v_strides[1],
                 out.data_ptr(),
                 heads * head_dim,
                 head_dim,
                 tokens,
                 heads,
                 num_kv_heads,
-                plan.page_size,
+                lease.page_size(),
                 dtype_code(q.kind())?,
                 stream_of(q.device()),
             )
