@@ -45,6 +45,54 @@ TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "prof
                                "decode_cfg2_traffic.txt")
 
 
+def host_threads() -> int:
+    """Threads for the CPU baselines: the process's share of the host's cores. The GPU box
+    gives one GPU's job a 16-CPU share (exported as OMP_NUM_THREADS) whatever os.cpu_count()
+    reports for the whole host, so the share, not the host count, is what runs without
+    oversubscription; both are recorded by ``host_cpu``."""
+    share = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None
+    env = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return max(1, min(x for x in (share, env or None, os.cpu_count() or 1) if x))
+
+
+def host_cpu(threads: int) -> dict:
+    """The host CPU a baseline ran on: lscpu's model name, os.cpu_count(), the CPUs this
+    process may run on, and the threads torch and the numpy BLAS actually use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    info = {"model": model, "os_cpu_count": os.cpu_count(),
+            "affinity_cpus": (len(os.sched_getaffinity(0))
+                              if hasattr(os, "sched_getaffinity") else None),
+            "threads": threads, "torch_threads": torch.get_num_threads()}
+    try:
+        from threadpoolctl import threadpool_info
+        info["blas_threads"] = sorted({p.get("num_threads") for p in threadpool_info()
+                                       if p.get("user_api") == "blas"})
+    except Exception:  # threadpoolctl absent: the env var is what the BLAS read at load
+        info["blas_threads"] = os.environ.get("OPENBLAS_NUM_THREADS") or os.environ.get(
+            "OMP_NUM_THREADS")
+    return info
+
+
+def set_host_threads() -> int:
+    """Applies ``host_threads()`` to torch and to the numpy BLAS; returns the count."""
+    threads = host_threads()
+    torch.set_num_threads(threads)
+    try:
+        from threadpoolctl import threadpool_limits
+        threadpool_limits(threads)
+    except Exception:
+        pass
+    return threads
+
+
 def measured_traffic():
     """HBM bytes per decode launch from the committed rocprofv3 --pmc summary, if any."""
     try:
@@ -89,6 +137,19 @@ def e2e_section(dev, args) -> dict:
     wall = time.perf_counter() - t0
     ttft = sorted((r.first_token_time - r.arrival) * 1e3 for r in reqs)
     out_tokens = sum(len(r.output) for r in reqs)
+    # Properties of the full-size run (after the timed region): every request produced its
+    # whole budget of in-vocabulary tokens, every KV page came back, and every decode step
+    # was a graph replay. A plumbing bug fails the bench here rather than passing silently.
+    checks = {
+        "all_outputs_full_length": all(len(r.output) == n_out for r in reqs),
+        "all_tokens_in_vocab": all(0 <= t < cfg.vocab_size for r in reqs for t in r.output),
+        "all_pages_returned": len(eng.pages.free) == eng.pool.layout.num_pages,
+        "every_decode_step_a_graph_replay": (eng.stats["graph_steps"]
+                                             == eng.stats["decode_steps"] > 0),
+    }
+    failed = [k for k, ok in checks.items() if not ok]
+    if failed:
+        raise AssertionError(f"e2e run failed its output checks: {failed}")
     result = {
         "output_tok_s": round(out_tokens / wall, 1),
         "p50_ttft_ms": round(statistics.median(ttft), 1),
@@ -99,6 +160,7 @@ def e2e_section(dev, args) -> dict:
         "prefill_batches": eng.stats["prefill_batches"],
         "decode_steps": eng.stats["decode_steps"],
         "graph_steps": eng.stats["graph_steps"],
+        "checks": checks,
         "setup_s": round(setup_s, 1),
         "config": {"model": "Qwen3-8B shape (random bf16 N(0,0.02) weights)",
                    "layers": cfg.num_layers, "requests": n_req, "input": n_in,
@@ -132,6 +194,7 @@ def e2e_cpu_baseline(seed: int) -> dict:
     prompt = np.random.default_rng(seed).integers(0, cfg8.vocab_size, 1024)
     steps = 8
     times = {}
+    threads = set_host_threads()
     for layers, cfg, w in ((1, cfg1, w1), (2, cfg2, w2)):
         m = oq.Qwen3Oracle(cfg, w)
         t0 = time.perf_counter()
@@ -151,9 +214,9 @@ def e2e_cpu_baseline(seed: int) -> dict:
         return times[1][i] - per_layer + cfg8.num_layers * per_layer
 
     ttft_s, token_s = at_36(0), at_36(1)
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
     return {"value": round(1.0 / token_s, 3), "unit": "output tok/s (one request)",
             "ttft_ms": round(ttft_s * 1e3, 1), "cores": threads, "kind": "port",
+            "host": host_cpu(threads),
             "sample": ("numpy fp32 restatement of the reference CPU eager forward at the "
                        "Qwen3-8B widths, one request: 1024-token prefill + 8 decode steps "
                        "timed at 1 and 2 layers, fixed + per-layer parts extrapolated to 36 "
@@ -237,8 +300,7 @@ def cpu_baseline(w, requests: int):
     """Oracle's torch-CPU fp32 restatement of the reference decode path on a sample."""
     from oracle import attention as oatt
 
-    threads = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
+    threads = set_host_threads()
     idx = list(range(requests))
     lens = [int(w["lengths"][i]) for i in idx]
     # Compact CPU pool holding only the sampled requests' slots (same gather pattern).
@@ -262,6 +324,7 @@ def cpu_baseline(w, requests: int):
     sec = statistics.median(times)
     nbytes = decode_bytes(torch.tensor(lens), w["HQ"], w["HKV"], w["D"])
     return {"value": nbytes / sec / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "host": host_cpu(threads),
             "sample": f"{len(idx)} of 64 requests ({sum(lens)} KV tokens), libtorch fp32 CPU "
                       "decode_with_cache restatement, median of 5"}
 
@@ -350,8 +413,7 @@ def replan_section(dev) -> dict:
 
 def _cpu_median_ms(fn, runs: int = 3) -> tuple[float, int]:
     """Median wall time of ``fn`` on the host cores (one warm-up run), and the threads used."""
-    threads = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
+    threads = set_host_threads()
     fn()
     times = []
     for _ in range(runs):
@@ -403,7 +465,7 @@ def prefill_sections(dev, reps: int, cpu: bool = True) -> dict:
         cms, threads = _cpu_median_ms(lambda: oatt.prefill_ragged_torch(qs, ks, vs, sb))
         sflops = 4 * 16 * 128 * sum(int(x) * (int(x) + 1) // 2 for x in lens[:2])
         out["prefill_ragged_cfg3"]["cpu_baseline"] = {
-            "value": round(sflops / (cms * 1e-3) / 1e9, 2), "unit": "GFLOP/s", "cores": threads,
+            "value": round(sflops / (cms * 1e-3) / 1e9, 2), "unit": "GFLOP/s", "cores": threads, "host": host_cpu(threads),
             "kind": "port", "sample": f"first 2 of 8 sequences ({sb[-1]} tokens), torch-CPU fp32 "
                                       "SDPA prefill restatement, median of 3"}
     del plan
@@ -465,7 +527,7 @@ def prefill_sections(dev, reps: int, cpu: bool = True) -> dict:
         sflops = 4 * 32 * 128 * sum(int(ext[r]) * int(pref[r]) +
                                     int(ext[r]) * (int(ext[r]) + 1) // 2 for r in rows)
         out["prefill_paged_cfg4"]["cpu_baseline"] = {
-            "value": round(sflops / (cms * 1e-3) / 1e9, 2), "unit": "GFLOP/s", "cores": threads,
+            "value": round(sflops / (cms * 1e-3) / 1e9, 2), "unit": "GFLOP/s", "cores": threads, "host": host_cpu(threads),
             "kind": "port", "sample": f"2 of 16 requests ({sb[-1]} extend tokens over "
                                       f"{int(pref[rows].sum())} cached), torch-CPU fp32 "
                                       "restatement, median of 3"}
@@ -714,7 +776,7 @@ def serving_ops_section(dev, reps: int, cpu: bool = True) -> dict:
             cms, threads = _cpu_median_ms(cpu_pass)
             cbytes = n * 128 * 2 * (32 * 2 + 8 * 2 + 8 + 16) + 16 * n
             res["cpu_baseline"] = {
-                "value": round(cbytes / (cms * 1e-3) / 1e9, 2), "unit": "GB/s", "cores": threads,
+                "value": round(cbytes / (cms * 1e-3) / 1e9, 2), "unit": "GB/s", "cores": threads, "host": host_cpu(threads),
                 "kind": "port", "sample": f"{n} of the {t} tokens, torch-CPU / numpy restatement "
                                           "(ops.rs:39-51, 84-97, base.rs:123-151), median of 3"}
         out[name] = res
@@ -781,7 +843,7 @@ def serving_ops_section(dev, reps: int, cpu: bool = True) -> dict:
             wc = sets[0]["qkv" if nm == "qkv_norm_rope_store" else nm].float().cpu()
             cms, threads = _cpu_median_ms(lambda: xc @ wc.T)
             res["cpu_baseline"] = {"value": round(2 * 16 * n * kk / (cms * 1e-3) / 1e9, 2),
-                                   "unit": "GFLOP/s", "cores": threads, "kind": "port",
+                                   "unit": "GFLOP/s", "cores": threads, "host": host_cpu(threads), "kind": "port",
                                    "sample": "16 of the 256 rows, torch-CPU fp32 x @ w^T "
                                              "(linear.rs:5-7), median of 3"}
         out[f"linear_256_{nm}"] = res
@@ -875,7 +937,7 @@ def norm_sections(dev, reps: int, cpu: bool = True) -> dict:
             cms, threads = _cpu_median_ms(fn)
             res[name]["cpu_baseline"] = {
                 "value": round(res[name]["bytes"] / (cms * 1e-3) / 1e9, 2), "unit": "GB/s",
-                "cores": threads, "kind": "port",
+                "cores": threads, "host": host_cpu(threads), "kind": "port",
                 "sample": "full rows, torch-CPU restatement of ops.rs, median of 3"}
     return res
 
@@ -1005,7 +1067,7 @@ def main():
         cms, threads = _cpu_median_ms(lambda: (kpool.index_copy_(0, cloc, kn),
                                                vpool.index_copy_(0, cloc, vn)), runs=21)
         result["kv_store"]["cpu_baseline"] = {
-            "value": round(sbytes / (cms * 1e-3) / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "value": round(sbytes / (cms * 1e-3) / 1e9, 3), "unit": "GB/s", "cores": threads, "host": host_cpu(threads),
             "kind": "port", "sample": "64 rows into a 65,536-slot CPU pool, median of 21"}
     # Small kernels by graph replay (device time per launch, no Python launch overhead).
     kv_graph_us = _graph_time_us(lambda: caches[0].write_kv(w["knew"], w["vnew"], w["loc"]))

@@ -309,7 +309,8 @@ extern "C" const char* mi355x_rope(void* q, void* k, const int64_t* positions, c
 
 namespace {
 // The QK-norm -> RoPE -> K/V store pass; with `part` its q/k/v rows come from split-K
-// partials (see HeadArgs) and v is also written to `v_out` (same strides as v).
+// partials (see HeadArgs) and v is also written to `v_out` (same strides as v). With
+// `check_only` it validates the arguments and launches nothing.
 const char* qk_rows_impl(
     void* q, void* k, const void* v, const void* q_weight, const void* k_weight,
     const int64_t* positions, const float* cos, const float* sin, int64_t max_positions,
@@ -317,7 +318,7 @@ const char* qk_rows_impl(
     int64_t reserved, int32_t* error_count, int64_t tokens, int64_t q_heads, int64_t k_heads,
     int64_t width, int64_t q_token_stride, int64_t q_head_stride, int64_t k_token_stride,
     int64_t k_head_stride, int64_t v_token_stride, int64_t v_head_stride, double eps, int dtype,
-    void* stream, const float* part, int32_t part_splits) {
+    void* stream, const float* part, int32_t part_splits, bool check_only = false) {
   if (tokens < 0 || q_heads < 0 || k_heads < 0 || max_positions < 0 || capacity < 0)
     return set_error("mi355x_qk_norm_rope_store: bad shape");
   if (width != kHeadDim) return set_error("mi355x_qk_norm_rope_store: width must be 128");
@@ -380,6 +381,7 @@ const char* qk_rows_impl(
   if (!ok)
     return set_error(
         "mi355x_qk_norm_rope_store: views must be 16-byte aligned with strides divisible by 8");
+  if (check_only) return nullptr;
   auto s = static_cast<hipStream_t>(stream);
   if (dtype == 0)
     launch_rows_dt<0>(a, norm, rope, store, index64, s);
@@ -417,12 +419,22 @@ extern "C" const char* mi355x_linear_qk_norm_rope_store(
     return set_error("mi355x_linear_qk_norm_rope_store: needs norm weights, positions and a cache");
   const int64_t N = (q_heads + 2 * k_heads) * kHeadDim;
   if (ldo < N) return set_error("mi355x_linear_qk_norm_rope_store: ldo < (Hq + 2 Hkv) * 128");
+  if (workspace && !aligned(workspace, 16))
+    return set_error("mi355x_linear_qk_norm_rope_store: workspace must be 16-byte aligned");
+  auto* base = static_cast<uint16_t*>(qkv);
+  // Every argument of the pass is checked before the projection is queued, so a refused
+  // call launches nothing (and leaves no unreduced split-K partials behind).
+  if (const char* e = qk_rows_impl(
+          base, base + q_heads * kHeadDim, base + (q_heads + k_heads) * kHeadDim, q_weight,
+          k_weight, positions, cos, sin, max_positions, k_cache, v_cache, loc, index64,
+          capacity, reserved, error_count, M, q_heads, k_heads, kHeadDim, ldo, kHeadDim, ldo,
+          kHeadDim, ldo, kHeadDim, eps, dtype, stream, nullptr, 0, true))
+    return e;
   auto s = static_cast<hipStream_t>(stream);
   int used = 1;
   if (const char* e = run_linear(x, ldx, w, ldw, qkv, ldo, M, N, K, workspace, workspace_bytes,
                                  cus, -1, -1, dtype, true, &used, s))
     return e;
-  auto* base = static_cast<uint16_t*>(qkv);
   return qk_rows_impl(base, base + q_heads * kHeadDim, base + (q_heads + k_heads) * kHeadDim,
                       q_weight, k_weight, positions, cos, sin, max_positions, k_cache, v_cache,
                       loc, index64, capacity, reserved, error_count, M, q_heads, k_heads,

@@ -11,9 +11,15 @@ Restates src/models/qwen3/model.rs:155-534 with the `pt` attention backend
 
 Weights are a dict of float32 arrays with the Hugging Face names used by
 ``llm_infer_rust_amd.model.Qwen3Model.named_parameters`` (qkv and gate/up packed).
-Pinned by the reference's self-consistency fixture (model.rs:730-900): prefill + cached decode
-gives the same logits as a full forward over the whole sequence, and chunked prefill the same as
-one-shot prefill; and by the attention / norm / RoPE oracles it is built from.
+Pinned by Hugging Face `transformers`' own Qwen3ForCausalLM (an independent implementation of
+the same architecture) on seeded random weights with non-unit norm weights: prompt + cached
+decode logits within 1e-4 at two tiny shapes (tied / untied head, rope_theta 1e4 / 1e6, GQA
+group 2 / 4) and at 2 layers of the Qwen3-0.6B widths (tests/test_oracle_qwen3_hf.py, whose
+mutation tests show that QK-norm after RoPE, a post-attention norm without the residual, a
+wrong rope_theta or a tied/untied mix-up each fail it); by the reference's self-consistency
+fixture (model.rs:730-900): prefill + cached decode gives the same logits as a full forward
+over the whole sequence, and chunked prefill the same as one-shot prefill; and by the
+attention / norm / RoPE oracles it is built from.
 """
 from __future__ import annotations
 
@@ -104,9 +110,18 @@ class Qwen3Oracle:
         return tokens, min(margins) if margins else float("inf")
 
 
-def random_weights(cfg, seed: int, std: float = 0.02) -> dict[str, np.ndarray]:
-    """Seeded N(0, std) float32 matrices with unit norm weights, Hugging Face names."""
+def random_weights(cfg, seed: int, std: float = 0.02,
+                   norm_range: tuple[float, float] | None = None) -> dict[str, np.ndarray]:
+    """Seeded N(0, std) float32 matrices, Hugging Face names. Norm weights are 1, or, with
+    ``norm_range``, U(lo, hi) from a second generator (seed + 1) so the matrices are the same
+    either way; non-unit norm weights make a swapped or misplaced norm visible."""
     rng = np.random.default_rng(seed)
+    nrng = np.random.default_rng(seed + 1)
+
+    def normw(n):
+        if norm_range is None:
+            return np.ones(n, np.float32)
+        return nrng.uniform(norm_range[0], norm_range[1], n).astype(np.float32)
     h, d, f = cfg.hidden_size, cfg.head_dim, cfg.intermediate_size
     qkv = (cfg.num_attention_heads + 2 * cfg.num_kv_heads) * d
 
@@ -114,17 +129,17 @@ def random_weights(cfg, seed: int, std: float = 0.02) -> dict[str, np.ndarray]:
         return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
 
     w = {"model.embed_tokens.weight": mat(cfg.vocab_size, h),
-         "model.norm.weight": np.ones(h, np.float32)}
+         "model.norm.weight": normw(h)}
     if not cfg.tie_word_embeddings:
         w["lm_head.weight"] = mat(cfg.vocab_size, h)
     for i in range(cfg.num_layers):
         p = f"model.layers.{i}."
-        w[p + "input_layernorm.weight"] = np.ones(h, np.float32)
+        w[p + "input_layernorm.weight"] = normw(h)
         w[p + "self_attn.qkv_proj.weight"] = mat(qkv, h)
-        w[p + "self_attn.q_norm.weight"] = np.ones(d, np.float32)
-        w[p + "self_attn.k_norm.weight"] = np.ones(d, np.float32)
+        w[p + "self_attn.q_norm.weight"] = normw(d)
+        w[p + "self_attn.k_norm.weight"] = normw(d)
         w[p + "self_attn.o_proj.weight"] = mat(h, cfg.num_attention_heads * d)
-        w[p + "post_attention_layernorm.weight"] = np.ones(h, np.float32)
+        w[p + "post_attention_layernorm.weight"] = normw(h)
         w[p + "mlp.gate_up_proj.weight"] = mat(2 * f, h)
         w[p + "mlp.down_proj.weight"] = mat(h, f)
     return w

@@ -164,6 +164,40 @@ def test_fused_qkv_projection_pass_equals_the_two_steps(gpu, dtype, tokens, hq, 
         assert splits_bytes > 0  # the partials route is the one exercised here
 
 
+def test_fused_qkv_route_refuses_before_launching(gpu):
+    """An argument the pass would refuse (here: no v_cache) is reported before the projection
+    is queued: qkv keeps its contents and the cache is untouched."""
+    from llm_infer_rust_amd import _native
+    from llm_infer_rust_amd._native import lib
+
+    tokens, hq, hkv, hidden = 256, 32, 8, 4096
+    n = (hq + 2 * hkv) * 128
+    x = torch.randn(tokens, hidden, device=gpu).to(torch.bfloat16)
+    w = (torch.randn(n, hidden, device=gpu) * 0.02).to(torch.bfloat16)
+    qw = torch.ones(128, dtype=torch.bfloat16, device=gpu)
+    pos = torch.arange(tokens, device=gpu)
+    rope = ops.HalfSplitRope(4096, 128, 1_000_000.0, gpu)
+    att = bound_attention(512, 16, hkv, torch.bfloat16, gpu, 0)
+    loc = torch.arange(1, tokens + 1, dtype=torch.int64, device=gpu)
+    cus = _native.device_cus(x.device)
+    need = lib().mi355x_linear_workspace_bytes(tokens, n, hidden, cus, -1, -1)
+    assert need > 0  # the split-K route, whose partials a refused pass would strand
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    qkv = torch.full((tokens, n), 7.0, dtype=torch.bfloat16, device=gpu)
+    before = att.k_cache.clone()
+    kc, _ = att.cache_tensors()
+    err = lib().mi355x_linear_qk_norm_rope_store(
+        x.data_ptr(), hidden, w.data_ptr(), hidden, qkv.data_ptr(), n, tokens, hidden, hq, hkv,
+        ws.data_ptr(), need, cus, qw.data_ptr(), qw.data_ptr(), pos.data_ptr(),
+        rope.cos.data_ptr(), rope.sin.data_ptr(), rope.max_positions, kc.data_ptr(), None,
+        loc.data_ptr(), True, kc.size(0) * kc.size(1), 0, None, 1e-6, 0,
+        torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert err is not None and b"v_cache" in err
+    assert bool((qkv == 7.0).all())
+    assert torch.equal(att.k_cache, before)
+
+
 def test_fused_pass_reports_out_of_range_slot(gpu):
     _, q, k, v = packed_qkv(4, 16, 8, torch.bfloat16, gpu, 5)
     att = bound_attention(8, 1, 8, torch.bfloat16, gpu, -1)

@@ -35,8 +35,10 @@ def test_noalloc_linear_matches_workspace_linear(gpu):
     stream = torch.cuda.current_stream().cuda_stream
     g = torch.Generator().manual_seed(5)
     # QKV of a Qwen3-8B decode step at 256 rows (split K), then a smaller o_proj-like call.
+    needs = {}
     for m, n, k in ((256, 6144, 4096), (64, 4096, 4096), (37, 1024, 4096)):
         need = lib.mi355x_linear_workspace_bytes(m, n, k, cus, -1, -1)
+        needs[m] = need
         print(f"[noalloc] m={m} n={n} k={k} split-K bytes={need}", flush=True)
         x = torch.randn(m, k, generator=g).to(torch.bfloat16).to(gpu)
         w = (torch.randn(n, k, generator=g) * 0.05).to(torch.bfloat16).to(gpu)
@@ -48,7 +50,8 @@ def test_noalloc_linear_matches_workspace_linear(gpu):
         assert err is None, err
         torch.cuda.synchronize()
         assert torch.equal(got, want), (m, n, k)
-    assert need > 0 or m < 256  # at least the first call went through the scratch
+    # The 256-row QKV call splits K, so its partials went through the scratch array.
+    assert needs[256] > 0, needs
 
 
 def test_noalloc_linear_refuses_oversized_partials(gpu):
