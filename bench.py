@@ -120,54 +120,69 @@ def e2e_section(dev, args) -> dict:
     t0 = time.perf_counter()
     model = Qwen3Model(cfg, torch.bfloat16, dev).init_random(seed=args.seed)
     n_req, n_in, n_out = args.e2e_requests, args.e2e_input, args.e2e_output
-    eng = Engine(model, EngineConfig(page_size=16, max_running_req=256,
-                                     max_prefill_tokens_per_batch=8192,
-                                     max_seq_len=n_in + n_out, seed=args.seed))
-    torch.cuda.synchronize()
-    setup_s = time.perf_counter() - t0
     rng = np.random.default_rng(args.seed)
     params = SamplingParams(temperature=0.7, top_k=50, top_p=0.9, ignore_eos=True,
                             max_tokens=n_out)
     prompts = [rng.integers(0, cfg.vocab_size, n_in) for _ in range(n_req)]
+
+    def serve(use_graphs: bool) -> dict:
+        eng = Engine(model, EngineConfig(page_size=16, max_running_req=256,
+                                         max_prefill_tokens_per_batch=8192,
+                                         max_seq_len=n_in + n_out, seed=args.seed,
+                                         use_graphs=use_graphs))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        reqs = [eng.add_request(p, params) for p in prompts]
+        eng.run_until_complete()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ttft = sorted((r.first_token_time - r.arrival) * 1e3 for r in reqs)
+        out_tokens = sum(len(r.output) for r in reqs)
+        # Properties of the full-size run (after the timed region): every request produced
+        # its whole budget of in-vocabulary tokens, every KV page came back, and with graphs
+        # every decode step was a graph replay. A plumbing bug fails the bench here rather
+        # than passing silently.
+        checks = {
+            "all_outputs_full_length": all(len(r.output) == n_out for r in reqs),
+            "all_tokens_in_vocab": all(0 <= t < cfg.vocab_size for r in reqs for t in r.output),
+            "all_pages_returned": len(eng.pages.free) == eng.pool.layout.num_pages,
+        }
+        if use_graphs:
+            checks["every_decode_step_a_graph_replay"] = (
+                eng.stats["graph_steps"] == eng.stats["decode_steps"] > 0)
+        failed = [k for k, ok in checks.items() if not ok]
+        if failed:
+            raise AssertionError(f"e2e run failed its output checks: {failed}")
+        out = {"output_tok_s": round(out_tokens / wall, 1),
+               "p50_ttft_ms": round(statistics.median(ttft), 1),
+               "p90_ttft_ms": round(ttft[int(0.9 * (len(ttft) - 1))], 1),
+               "wall_s": round(wall, 3), "output_tokens": out_tokens,
+               "prefill_batches": eng.stats["prefill_batches"],
+               "decode_steps": eng.stats["decode_steps"],
+               "graph_steps": eng.stats["graph_steps"], "checks": checks}
+        del eng
+        torch.cuda.empty_cache()
+        return out
+
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    reqs = [eng.add_request(p, params) for p in prompts]
-    eng.run_until_complete()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ttft = sorted((r.first_token_time - r.arrival) * 1e3 for r in reqs)
-    out_tokens = sum(len(r.output) for r in reqs)
-    # Properties of the full-size run (after the timed region): every request produced its
-    # whole budget of in-vocabulary tokens, every KV page came back, and every decode step
-    # was a graph replay. A plumbing bug fails the bench here rather than passing silently.
-    checks = {
-        "all_outputs_full_length": all(len(r.output) == n_out for r in reqs),
-        "all_tokens_in_vocab": all(0 <= t < cfg.vocab_size for r in reqs for t in r.output),
-        "all_pages_returned": len(eng.pages.free) == eng.pool.layout.num_pages,
-        "every_decode_step_a_graph_replay": (eng.stats["graph_steps"]
-                                             == eng.stats["decode_steps"] > 0),
-    }
-    failed = [k for k, ok in checks.items() if not ok]
-    if failed:
-        raise AssertionError(f"e2e run failed its output checks: {failed}")
+    setup_s = time.perf_counter() - t0
+    graph = serve(True)  # the config-5 run: hipGraph-captured decode
     result = {
-        "output_tok_s": round(out_tokens / wall, 1),
-        "p50_ttft_ms": round(statistics.median(ttft), 1),
-        "p90_ttft_ms": round(ttft[int(0.9 * (len(ttft) - 1))], 1),
-        "wall_s": round(wall, 3),
-        "output_tokens": out_tokens,
+        **graph,
         "input_tokens": n_req * n_in,
-        "prefill_batches": eng.stats["prefill_batches"],
-        "decode_steps": eng.stats["decode_steps"],
-        "graph_steps": eng.stats["graph_steps"],
-        "checks": checks,
         "setup_s": round(setup_s, 1),
         "config": {"model": "Qwen3-8B shape (random bf16 N(0,0.02) weights)",
                    "layers": cfg.num_layers, "requests": n_req, "input": n_in,
                    "output": n_out, "page_size": 16, "max_prefill_tokens": 8192,
                    "sampling": "T0.7 k50 p0.9 seed %d" % args.seed},
     }
-    del eng, model
+    if not getattr(args, "e2e_graph_only", False):
+        # The same serving run with the decode step launched eagerly (no graph), reported
+        # beside the graph figure on the same box.
+        eager = serve(False)
+        result["eager_decode"] = {k: eager[k] for k in ("output_tok_s", "p50_ttft_ms",
+                                                          "p90_ttft_ms", "wall_s")}
+    del model
     torch.cuda.empty_cache()
     if not getattr(args, "no_cpu_baseline", False):
         result["cpu_baseline"] = e2e_cpu_baseline(args.seed)
@@ -224,6 +239,38 @@ def e2e_cpu_baseline(seed: int) -> dict:
                        f"decode {times[1][1] * 1e3:.0f} / {times[2][1] * 1e3:.0f} ms per token)")}
 
 
+def summarize_kernel_trace(path: str, top: int = 40) -> str:
+    """Per-(kernel, grid) launch statistics from a rocprofv3 kernel_trace.csv: kernels that
+    run at several shapes (one prefill template serves config 4 and the long-prefix
+    continuation, for example) get a row per grid size, which the profiler's own stats merge.
+    Host-side text processing only (no GPU)."""
+    import csv
+    import re
+
+    rows: dict = {}
+    total = 0.0
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            grid = int(r.get("Grid_Size_X", 0) or 0) * int(r.get("Grid_Size_Y", 1) or 1) * int(
+                r.get("Grid_Size_Z", 1) or 1)
+            name = r["Kernel_Name"].replace("void ", "", 1)
+            name = name.replace("mi355x::(anonymous namespace)::", "")
+            name = re.sub(r"\(anonymous namespace\)::", "", name)
+            name = re.sub(r"\(.*", "", name)
+            rows.setdefault((name[:70], grid), []).append(dur)
+            total += dur
+    lines = [f"{'kernel':70s} {'grid':>10s} {'calls':>7s} {'avg_us':>9s} {'median_us':>9s} "
+             f"{'min_us':>8s} {'max_us':>8s} {'share%':>7s}"]
+    ranked = sorted(rows.items(), key=lambda kv: -sum(kv[1]))[:top]
+    for (name, grid), d in ranked:
+        d = sorted(d)
+        lines.append(f"{name:70s} {grid:10d} {len(d):7d} {sum(d) / len(d):9.2f} "
+                     f"{d[len(d) // 2]:9.2f} {d[0]:8.2f} {d[-1]:8.2f} "
+                     f"{100 * sum(d) / total:7.2f}")
+    return "\n".join(lines)
+
+
 METRIC = "decode-attn HBM GB/s (% peak); prefill MFMA util; output tok/s Qwen3-8B"
 
 
@@ -246,6 +293,11 @@ def parse_args():
     p.add_argument("--e2e-layers", type=int, default=None,
                    help="override the layer count (smoke runs only; the reported config is 36)")
     p.add_argument("--skip-e2e", action="store_true")
+    p.add_argument("--summarize-kernel-trace", metavar="CSV",
+                   help="print per-(kernel, grid) statistics of a rocprofv3 kernel_trace.csv "
+                        "and exit (host only)")
+    p.add_argument("--e2e-graph-only", action="store_true",
+                   help="skip the eager-decode comparison run of the e2e section")
     p.add_argument("--copy-calibration", action="store_true",
                    help="run one 256 MiB device-to-device copy first (PMC byte-count "
                         "calibration for FETCH_SIZE / WRITE_SIZE)")
@@ -560,14 +612,14 @@ def prefill_sections(dev, reps: int, cpu: bool = True) -> dict:
 
 
 def ceilings_section(dev, w, reps: int) -> dict:
-    """Measured ceilings of this GPU for the two bounds (llm_infer_rust_amd/calib/ceilings.hip):
+    """Measured ceilings of this GPU for the two bounds (ceilings/ceilings.hip):
     the cfg2 decode memory pattern without arithmetic (random 2 KiB K and V rows at the same
     slots, rotating over the same 4 pools), a contiguous read of the same byte count, bf16 MFMA
     on random operands, and the prefill kernel's per-tile work on LDS-resident random tiles."""
     import ctypes
     from llm_infer_rust_amd import _native  # noqa: F401  (HIP runtime loaded by torch first)
     lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)),
-                                   "llm_infer_rust_amd", "libmi355x_calib.so"))
+                                   "ceilings", "libmi355x_calib.so"))
     for name in ("mi355x_calib_gather", "mi355x_calib_stream", "mi355x_calib_mfma",
                  "mi355x_calib_attention_core"):
         getattr(lib, name).restype = ctypes.c_char_p
@@ -944,6 +996,9 @@ def norm_sections(dev, reps: int, cpu: bool = True) -> dict:
 
 def main():
     args = parse_args()
+    if args.summarize_kernel_trace:
+        print(summarize_kernel_trace(args.summarize_kernel_trace))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
         sys.exit(2)

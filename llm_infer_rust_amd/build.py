@@ -17,9 +17,6 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = CSRC / "_build"
 LIB = PKG / "libmi355x_attn.so"
-# Measurement-only library (hardware ceilings for bench.py); never loaded by the product.
-CALIB_SRC = PKG / "calib" / "ceilings.hip"
-CALIB_LIB = PKG / "libmi355x_calib.so"
 INCLUDE = PKG.parent / "include"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -76,19 +73,7 @@ def build(jobs: int | None = None) -> Path:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, LIB)
-    build_calib()
     return LIB
-
-
-def build_calib() -> Path:
-    """Compile the measurement-only ceilings library."""
-    tmp = CALIB_LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, *COMMON_FLAGS, "-shared", str(CALIB_SRC), "-o", str(tmp)]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {CALIB_SRC.name}:\n{proc.stderr}")
-    os.replace(tmp, CALIB_LIB)
-    return CALIB_LIB
 
 
 if __name__ == "__main__":
