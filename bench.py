@@ -271,6 +271,39 @@ def summarize_kernel_trace(path: str, top: int = 40) -> str:
     return "\n".join(lines)
 
 
+def summarize_counters(paths: list, match: str = "") -> str:
+    """Per-(kernel, grid) means of every counter in rocprofv3 --pmc counter_collection.csv
+    files (one file per counter pass; kernels whose name contains `match`). Host-side text
+    processing only (no GPU)."""
+    import csv
+    import re
+
+    acc: dict = {}
+    for path in paths:
+        per: dict = {}
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                name = r["Kernel_Name"].replace("void ", "", 1)
+                name = re.sub(r"\(anonymous namespace\)::", "", name.replace("mi355x::", ""))
+                name = re.sub(r"\(.*", "", name)
+                if match not in name:
+                    continue
+                key = (name[:70], int(r.get("Grid_Size", 0) or 0))
+                per.setdefault((r["Dispatch_Id"], key), {})[r["Counter_Name"]] = float(
+                    r["Counter_Value"])
+        for (_, key), counters in per.items():
+            for c, v in counters.items():
+                acc.setdefault(key, {}).setdefault(c, []).append(v)
+    lines = []
+    for (name, grid), counters in sorted(acc.items()):
+        n = max(len(v) for v in counters.values())
+        lines.append(f"{name}  grid {grid}  dispatches {n}")
+        for c in sorted(counters):
+            v = counters[c]
+            lines.append(f"    {c:36s} {sum(v) / len(v):18.1f}")
+    return "\n".join(lines)
+
+
 METRIC = "decode-attn HBM GB/s (% peak); prefill MFMA util; output tok/s Qwen3-8B"
 
 
@@ -296,6 +329,11 @@ def parse_args():
     p.add_argument("--summarize-kernel-trace", metavar="CSV",
                    help="print per-(kernel, grid) statistics of a rocprofv3 kernel_trace.csv "
                         "and exit (host only)")
+    p.add_argument("--summarize-counters", metavar="CSV", nargs="+",
+                   help="print per-(kernel, grid) means of rocprofv3 --pmc counter_collection "
+                        "CSVs and exit (host only; --counter-match filters kernel names)")
+    p.add_argument("--counter-match", default="", help="kernel-name filter for "
+                   "--summarize-counters")
     p.add_argument("--e2e-graph-only", action="store_true",
                    help="skip the eager-decode comparison run of the e2e section")
     p.add_argument("--copy-calibration", action="store_true",
@@ -998,6 +1036,9 @@ def main():
     args = parse_args()
     if args.summarize_kernel_trace:
         print(summarize_kernel_trace(args.summarize_kernel_trace))
+        return
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters, args.counter_match))
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
