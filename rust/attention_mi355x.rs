@@ -540,11 +540,10 @@ pub(super) fn mi355x_prefill(
     // Paged plans read the layer's whole cache [pages, page, kv_heads, 128] (row stride
     // kv_heads * 128, head stride 128); ragged plans read the (packed) K/V projection rows
     // in place with their own strides.
-    let layer_cache;
     let (k_src, v_src, k_strides, v_strides) = if *paged {
-        layer_cache = cache.cache_tensors()?;
+        let (k_cache, v_cache) = cache.cache_tensors()?;
         let row = num_kv_heads * head_dim;
-        (&layer_cache.0, &layer_cache.1, [row, head_dim], [row, head_dim])
+        (k_cache, v_cache, [row, head_dim], [row, head_dim])
     } else {
         let (ks, vs) = (k.stride(), v.stride());
         (k, v, [ks[0], ks[1]], [vs[0], vs[1]])
