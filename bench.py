@@ -178,7 +178,9 @@ def e2e_section(dev, args) -> dict:
     }
     if not getattr(args, "e2e_graph_only", False):
         # The same serving run with the decode step launched eagerly (no graph), reported
-        # beside the graph figure on the same box.
+        # beside the graph figure on the same box. The pause before it (outside both timed
+        # regions) separates the two runs in a kernel trace (--summarize-gaps).
+        time.sleep(0.5)
         eager = serve(False)
         result["eager_decode"] = {k: eager[k] for k in ("output_tok_s", "p50_ttft_ms",
                                                           "p90_ttft_ms", "wall_s")}
@@ -304,6 +306,49 @@ def summarize_counters(paths: list, match: str = "") -> str:
     return "\n".join(lines)
 
 
+def summarize_gaps(path: str, idle_s: float = 0.2) -> str:
+    """Idle time between consecutive kernels in a rocprofv3 kernel_trace.csv, per stretch of
+    activity (stretches are split at host pauses longer than `idle_s`). Run on a trace of
+    `--only e2e`, the two long stretches are the serving run with graph-replayed decode and
+    the one with eager decode. Host-side text processing only (no GPU)."""
+    import csv
+
+    spans = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            spans.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
+                          "decode_mma_kernel" in r["Kernel_Name"]))
+    spans.sort()
+    stretches, cur = [], []
+    for sp in spans:
+        if cur and sp[0] - max(e for _, e, _ in cur[-64:]) > idle_s * 1e9:
+            stretches.append(cur)
+            cur = []
+        cur.append(sp)
+    if cur:
+        stretches.append(cur)
+    lines = [f"{'stretch':>7s} {'kernels':>8s} {'decode_attn':>11s} {'span_s':>8s} {'busy_s':>8s} "
+             f"{'idle_%':>7s} {'gap_median_us':>13s} {'gap_mean_us':>11s}"]
+    for i, st in enumerate(stretches):
+        if len(st) < 1000:
+            continue
+        gaps, end = [], st[0][1]
+        busy = 0
+        for b, e, _ in st:
+            busy += e - b
+            if b > end:
+                gaps.append((b - end) / 1e3)
+            else:
+                gaps.append(0.0)
+            end = max(end, e)
+        gaps = sorted(gaps[1:])
+        span = (end - st[0][0]) / 1e9
+        lines.append(f"{i:7d} {len(st):8d} {sum(1 for x in st if x[2]):11d} {span:8.3f} "
+                     f"{busy / 1e9:8.3f} {100 * (1 - busy / 1e9 / span):7.2f} "
+                     f"{gaps[len(gaps) // 2]:13.2f} {sum(gaps) / len(gaps):11.2f}")
+    return "\n".join(lines)
+
+
 METRIC = "decode-attn HBM GB/s (% peak); prefill MFMA util; output tok/s Qwen3-8B"
 
 
@@ -334,6 +379,9 @@ def parse_args():
                         "CSVs and exit (host only; --counter-match filters kernel names)")
     p.add_argument("--counter-match", default="", help="kernel-name filter for "
                    "--summarize-counters")
+    p.add_argument("--summarize-gaps", metavar="CSV",
+                   help="print the idle time between consecutive kernels of a rocprofv3 "
+                        "kernel_trace.csv, per stretch of activity, and exit (host only)")
     p.add_argument("--e2e-graph-only", action="store_true",
                    help="skip the eager-decode comparison run of the e2e section")
     p.add_argument("--copy-calibration", action="store_true",
@@ -1036,6 +1084,9 @@ def main():
     args = parse_args()
     if args.summarize_kernel_trace:
         print(summarize_kernel_trace(args.summarize_kernel_trace))
+        return
+    if args.summarize_gaps:
+        print(summarize_gaps(args.summarize_gaps))
         return
     if args.summarize_counters:
         print(summarize_counters(args.summarize_counters, args.counter_match))

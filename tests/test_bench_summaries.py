@@ -40,3 +40,19 @@ def test_counter_summary_means_per_kernel_and_grid(tmp_path):
     assert "linear_kernel<0>  grid 98304  dispatches 2" in text
     assert "silu" not in text
     assert [ln.split()[-1] for ln in text.splitlines()[1:]] == ["20.0", "20.0"]
+
+
+def test_gap_summary_splits_stretches_at_host_pauses(tmp_path):
+    path = tmp_path / "kt.csv"
+    rows, t = [], 0
+    for gap_ns in (1000, 500):  # two serving runs: 1 us and 0.5 us between kernels
+        for i in range(1200):
+            rows.append(["decode_mma_kernel<0>" if i % 10 == 0 else "other", t, t + 5000])
+            t += 5000 + gap_ns
+        t += 10 ** 9  # a one-second host pause
+    _write(path, ["Kernel_Name", "Start_Timestamp", "End_Timestamp"], rows)
+    lines = bench.summarize_gaps(str(path)).splitlines()
+    assert len(lines) == 3
+    first, second = lines[1].split(), lines[2].split()
+    assert first[1] == second[1] == "1200" and first[2] == "120"
+    assert float(first[6]) == 1.0 and float(second[6]) == 0.5

@@ -96,3 +96,21 @@ def test_fused_qkv_route_checks_the_weight_shape():
     with pytest.raises(NativeError, match="q_heads \\+ 2 k_heads"):
         ops.linear_qk_norm_rope_store(x, torch.zeros(512, 64), 0, 2, None, None, 1e-6, None,
                                       None, None, None)
+
+
+def test_default_decode_graph_buckets():
+    """Decode graphs are captured for 1, 2, 4, 8 and every multiple of 8 up to the running
+    limit, so a partly filled step carries at most 7 pad rows; explicit sizes are kept."""
+    from llm_infer_rust_amd.engine import Engine, EngineConfig
+
+    eng = Engine.__new__(Engine)  # the bucket rule needs only the config
+    eng.cfg = EngineConfig()
+    sizes = eng._bucket_sizes()
+    assert sizes[:5] == [1, 2, 4, 8, 16] and sizes[-1] == 256 and len(sizes) == 35
+    assert all(b - a <= 8 for a, b in zip(sizes, sizes[1:]))
+    eng.cfg = EngineConfig(max_running_req=20)
+    assert eng._bucket_sizes() == [1, 2, 4, 8, 16, 20]
+    eng.cfg = EngineConfig(max_running_req=3)
+    assert eng._bucket_sizes() == [1, 2, 3]
+    eng.cfg = EngineConfig(graph_batch_sizes=(4, 1, 4))
+    assert eng._bucket_sizes() == [1, 4]
