@@ -162,3 +162,49 @@ def device_cus(device: torch.device) -> int:
     if index not in _CUS:
         _CUS[index] = torch.cuda.get_device_properties(index).multi_processor_count
     return _CUS[index]
+
+
+# ---------------------------------------------------------------------------
+# Releasing native plans. Dropping a plan frees device buffers and waits on its upload event
+# (hipFree, hipEventSynchronize), which a stream capture in progress does not allow: a plan
+# finalized by the garbage collector in the middle of a HIP graph capture would invalidate the
+# capture. Such a plan's handle is parked and released at the next safe point instead (the
+# next plan release or creation outside a capture, or an explicit release_deferred()).
+# ---------------------------------------------------------------------------
+_deferred: list[tuple[str, int]] = []
+_deferred_lock = threading.Lock()
+
+
+def _capturing() -> bool:
+    """True while this thread's current HIP stream is being captured into a graph."""
+    try:
+        return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+    except Exception:  # interpreter shutdown
+        return False
+
+
+def release_deferred() -> None:
+    """Release the plan handles parked during a capture (no-op while one is in progress)."""
+    if _capturing():
+        return
+    while True:
+        with _deferred_lock:
+            if not _deferred:
+                return
+            name, handle = _deferred.pop()
+        getattr(lib(), name)(handle)
+
+
+def release_handle(drop_entry: str, handle: int) -> None:
+    """Drop a native plan through `drop_entry` now, or after the capture in progress."""
+    if _capturing():
+        with _deferred_lock:
+            _deferred.append((drop_entry, handle))
+        return
+    release_deferred()
+    getattr(lib(), drop_entry)(handle)
+
+
+def deferred_count() -> int:
+    with _deferred_lock:
+        return len(_deferred)

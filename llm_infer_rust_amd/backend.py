@@ -28,6 +28,7 @@ from typing import Sequence
 import numpy as np
 import torch
 
+from . import _native
 from ._native import NativeError, check, dtype_code, last_error, lib, stream_of
 from .kv_cache import BaseAttention, ModelError
 
@@ -179,8 +180,8 @@ class DecodePlan:
 
     def __del__(self):
         if getattr(self, "handle", None):
-            try:
-                lib().mi355x_decode_plan_drop(self.handle)
+            try:  # deferred when a graph capture is in progress (see _native.release_handle)
+                _native.release_handle("mi355x_decode_plan_drop", self.handle)
             except Exception:  # interpreter shutdown
                 pass
             self.handle = None
@@ -189,6 +190,7 @@ class DecodePlan:
 def prepare_decode_plan(existing: DecodePlan | None, metadata: AttentionMetadata,
                         spec: AttentionSpec, page_size: int, graph: bool) -> DecodePlan:
     """``prepare_flashinfer_decode`` (backend.rs:574-640) on the native planner."""
+    _native.release_deferred()  # plans parked during a capture (outside one now)
     table = metadata.block_table
     lengths = metadata.cache_seqlens
     if table is None:

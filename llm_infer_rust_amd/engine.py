@@ -24,12 +24,14 @@ Mirrors the parts of the reference engine that feed the attention hot path:
 """
 from __future__ import annotations
 
+import gc
 import time
 from dataclasses import dataclass, field
 
 import numpy as np
 import torch
 
+from . import _native
 from .backend import AttentionMetadata, BatchPhase, DecodeHostMetadata
 from .batch import BatchContext, BatchRequest, DecodeBatch, DecodeRequest, DecodeTables
 from .kv_cache import KVCacheLayout, KVCachePool, ModelError
@@ -409,7 +411,23 @@ class Engine:
         return None
 
     def capture_graphs(self) -> None:
-        """Capture one decode step per bucket, largest first, sharing one memory pool."""
+        """Capture one decode step per bucket, largest first, sharing one memory pool.
+
+        Garbage is collected before the captures and the collector is paused during them: a
+        finalizer that calls into HIP (a native plan's release, for one) would otherwise be
+        able to run in the middle of a capture and invalidate it. Plans finalized anyway are
+        parked and released after the last capture (``_native.release_handle``)."""
+        gc.collect()
+        collecting = gc.isenabled()
+        gc.disable()
+        try:
+            self._capture_buckets()
+        finally:
+            if collecting:
+                gc.enable()
+            _native.release_deferred()
+
+    def _capture_buckets(self) -> None:
         model = self.model
         pool = torch.cuda.graph_pool_handle()
         for bs in sorted(self._bucket_sizes(), reverse=True):

@@ -14,6 +14,7 @@ import ctypes
 
 import torch
 
+from . import _native
 from ._native import check, dtype_code, last_error, lib, stream_of
 from .kv_cache import ModelError
 
@@ -50,15 +51,16 @@ class PrefillPlan:
 
     def __del__(self):
         if getattr(self, "handle", None):
-            try:
-                lib().mi355x_prefill_plan_drop(self.handle)
-            except Exception:
+            try:  # deferred when a graph capture is in progress (see _native.release_handle)
+                _native.release_handle("mi355x_prefill_plan_drop", self.handle)
+            except Exception:  # interpreter shutdown
                 pass
             self.handle = None
 
 
 def prepare_prefill_plan(existing: PrefillPlan | None, metadata, prefill, spec,
                          page_size: int) -> PrefillPlan:
+    _native.release_deferred()  # plans parked during a capture (outside one now)
     cu = metadata.cu_seqlens_q
     prefixes = metadata.prefix_lens
     table = metadata.block_table
