@@ -128,8 +128,9 @@ const char* mi355x_decode_plan_read(const void* plan, int32_t* indptr, int32_t* 
                                     void* stream);
 
 /* Host-only split-KV scheduler used by mi355x_decode_prepare (page size 1 view):
- * every workgroup of the grid takes an equal share of all tokens (`chunk_tokens`
- * receives the share); each request a share touches becomes one work item.
+ * every workgroup of the grid takes an equal share of the batch's kernel tiles plus
+ * a fixed cost per work item, cut on tile boundaries (`chunk_tokens` receives the
+ * share's tiles in tokens); each request a share touches becomes one work item.
  * Fills `work` (4 ints per item: request, token_begin, token_end, partial slot
  * or -1) and `merge` (2 ints per request: first partial slot or -1, item count).
  * Returns the item count, or -1 on invalid input / insufficient capacity.

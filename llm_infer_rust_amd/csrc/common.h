@@ -173,6 +173,12 @@ __device__ __forceinline__ void copy_to_lds(const void* src, uint32_t lds_base) 
                : "m0");
 }
 
+// One 4-byte global -> LDS copy per lane into lds_base + 4 * lane (same ordering rules).
+__device__ __forceinline__ void copy_dword_to_lds(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_base), "v"(src)
+               : "m0");
+}
+
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in 15:14).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

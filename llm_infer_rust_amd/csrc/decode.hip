@@ -31,6 +31,7 @@
 // decode_kernel (other head counts): one wave per kv head loads its 256-byte row
 // slices straight into registers.
 #include <algorithm>
+#include <functional>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -53,6 +54,7 @@ constexpr int kMaxWavesPerBlock = 8;
 constexpr int kDmaTile = 16;           // tokens per LDS tile
 constexpr int kDmaStages = 2;          // LDS ring depth
 constexpr int kDmaMaxEntries = 2048;   // page entries of one work item held in LDS
+static_assert(kDmaMaxEntries % 64 == 0, "entries are staged 64 at a time");
 constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------------------
@@ -104,15 +106,23 @@ struct DeviceBuffer {
 //   [o_work, +4*cap)     work items {request, token_begin, token_end, partial}
 //   [o_merge, +2*B)      per-request {first partial, chunk count}
 //   [o_wg, +wgs+1)       first work item of each workgroup
+//   [o_wgrec, +32*cap)   per-workgroup start record (kWgRec ints, 128-byte aligned):
+//                        {first item, item end, request, token_begin, token_end,
+//                         partial, page base, 0} of its first item, then the KV slots
+//                        of that item's first kDmaTile tokens (clamped to the item)
+constexpr int kWgRec = 32;
+constexpr int kWgRecSlots = 8;  // offset of the slots within a record
+static_assert(kWgRecSlots + kDmaTile <= kWgRec, "a start record holds one tile's slots");
 struct IntLayout {
-  int64_t o_indptr, o_work, o_merge, o_wg, total;
+  int64_t o_indptr, o_work, o_merge, o_wg, o_wgrec, total;
   static IntLayout make(int64_t rows, int64_t items_cap, int64_t wg_cap) {
     IntLayout l{};
     l.o_indptr = 4;
     l.o_work = (l.o_indptr + rows + 1 + 3) / 4 * 4;
     l.o_merge = l.o_work + 4 * items_cap;
     l.o_wg = l.o_merge + 2 * rows;
-    l.total = l.o_wg + wg_cap + 1;
+    l.o_wgrec = (l.o_wg + wg_cap + 1 + kWgRec - 1) / kWgRec * kWgRec;
+    l.total = l.o_wgrec + kWgRec * wg_cap;
     return l;
   }
 };
@@ -201,6 +211,7 @@ struct LaunchShape {
   int64_t grid_y;      // kv-head slices
   int64_t workgroups;  // split-KV workgroups per slice: the schedule's target
   int64_t max_item;    // most tokens of one work item
+  int64_t tile;        // tokens per kernel tile: the schedule's unit of work
   int64_t wg_capacity;
 };
 
@@ -220,11 +231,13 @@ LaunchShape launch_shape(int64_t cus, int64_t num_kv_heads, int64_t page_size) {
     const int64_t per_cu = std::max<int64_t>(1, (160 * 1024) / dma_lds_bytes(w));
     s.workgroups = std::max<int64_t>(1, cus * per_cu / s.grid_y);
     s.max_item = int64_t(kDmaMaxEntries - 1) * page_size;  // its page entries fit in LDS
+    s.tile = kDmaTile;
   } else {
     s.waves = waves_per_block(num_kv_heads);
     s.grid_y = (num_kv_heads + s.waves - 1) / s.waves;
     s.workgroups = target_items_for(cus, num_kv_heads);
     s.max_item = std::numeric_limits<int32_t>::max();
+    s.tile = kTileTokens;
   }
   // Every workgroup but the last takes more than share - 32 >= 3/4 share tokens.
   s.wg_capacity = s.workgroups + s.workgroups / 3 + 2;
@@ -237,51 +250,138 @@ int64_t items_capacity_for(const LaunchShape& s, int64_t rows, int64_t row_token
   return s.wg_capacity + rows * (1 + (row_tokens + s.max_item - 1) / s.max_item);
 }
 
-// Balanced split-KV ("stream-K" over the flattened token list): the workgroups of
-// the grid each take an equal share of all tokens, walking the requests in order, so
-// every workgroup streams the same number of rows and the grid drains at once. A
-// workgroup's share becomes one work item per request it touches; a request cut into
-// several items gets normalised partials that the merge kernel combines, one held by
-// a single item writes its output directly. A share boundary that would leave fewer
-// than 32 tokens of a request is moved to the request end, and an item holds at most
-// `max_item` tokens.
+// Balanced split-KV ("stream-K" over the flattened tile list): the workgroups of the
+// grid each take an equal share of the batch's work, walking the requests in order. Work
+// is counted in the kernel's tiles (`tile` tokens; a request's last tile may be partial)
+// plus a fixed cost per work item, because a workgroup's time is set by the tiles it
+// streams and the prologue of each item it starts (its page entries and query rows are
+// loaded before its first copies issue), and a workgroup holding more than its share
+// delays the whole launch. Cuts fall on tile boundaries, so no share pays for a partial
+// tile in the middle of a request. A workgroup's share becomes one work item per request
+// it touches; a request cut into several items gets normalised partials that the merge
+// kernel combines, one held by a single item writes its output directly. An item holds
+// at most `max_item` tokens.
 // Fills work (4 ints per item), merge (2 ints per request) and, when wg is not NULL,
 // wg[i] = first item of workgroup i (wg[workgroups] = item count). Returns the item
 // count, or -1 when a capacity is too small.
 int64_t schedule(const int32_t* lengths, int64_t batch, int64_t workgroups, int64_t max_item,
-                 int32_t* work, int64_t capacity, int32_t* merge, int64_t* share_out,
-                 int32_t* wg = nullptr, int64_t wg_capacity = 0, int64_t* wgs_out = nullptr) {
-  constexpr int64_t kMinShare = 128, kSliver = 32;
+                 int64_t tile, int32_t* work, int64_t capacity, int32_t* merge,
+                 int64_t* share_out, int32_t* wg = nullptr, int64_t wg_capacity = 0,
+                 int64_t* wgs_out = nullptr) {
+  constexpr int64_t kMinShareTokens = 128;
+  constexpr int64_t kUnit = 8;  // cost units per tile
+  // An item's prologue in cost units: 9/8 of a tile, as measured (per-workgroup end
+  // times at configs 2 and 5 fit 2.5-2.6 us per tile + 2.4-2.9 us per item). With it,
+  // requests of nearly equal length (the config-5 decode batches) are no longer cut
+  // just to even out a tile or two: 236.5 vs 244.4 us per launch there, and config 2
+  // within 0.3 us. Override with MI355X_DECODE_ITEM_COST (eighths of a tile; tuning
+  // knob, read once).
+  static const int64_t kItemCost = [] {
+    const char* env = std::getenv("MI355X_DECODE_ITEM_COST");
+    const long v = env ? std::strtol(env, nullptr, 10) : -1;
+    return v >= 0 ? static_cast<int64_t>(v) : int64_t(9);
+  }();
+  // The merge launch and the partials' traffic, in cost units (~2 tiles: config 5's
+  // decode launch takes 4.3 us longer with six requests split than with none).
+  constexpr int64_t kMergeCost = 16;
+  const int64_t max_item_tiles = std::max<int64_t>(1, max_item / tile);
   int64_t total = 0;
-  for (int64_t r = 0; r < batch; ++r) total += lengths[r];
-  int64_t share = std::max<int64_t>((total + workgroups - 1) / workgroups, kMinShare);
-  share = (share + kTileTokens - 1) / kTileTokens * kTileTokens;
-  int64_t items = 0, wgs = 0;
-  int64_t r = 0, pos = 0;
-  while (r < batch) {
-    if (wg) {
-      if (wgs >= wg_capacity) return -1;
-      wg[wgs] = static_cast<int32_t>(items);
-    }
-    ++wgs;
-    int64_t budget = share;
-    while (r < batch && budget > 0) {
-      const int64_t left = lengths[r] - pos;
-      int64_t take = std::min(budget, left);
-      if (left - take < kSliver) take = left;  // no sliver at the request end
-      take = std::min(take, max_item);
-      if (items >= capacity) return -1;
-      work[4 * items + 0] = static_cast<int32_t>(r);
-      work[4 * items + 1] = static_cast<int32_t>(pos);
-      work[4 * items + 2] = static_cast<int32_t>(pos + take);
-      ++items;
-      budget -= take;
-      pos += take;
-      if (pos == lengths[r]) {
-        ++r;
-        pos = 0;
+  for (int64_t r = 0; r < batch; ++r) total += (lengths[r] + tile - 1) / tile;
+  const int64_t min_share = std::max<int64_t>(1, kMinShareTokens / tile) * kUnit;
+  // Smallest share (cost units) whose walk needs at most `workgroups` workgroups: start
+  // from the tile-only bound and add item costs until the walk fits.
+  int64_t share = std::max((total * kUnit + workgroups - 1) / workgroups, min_share);
+  // One walk at a given share: 0 when it fits, 1 when it needs more than `wg_limit`
+  // workgroups, 2 when the item capacity is too small.
+  const int64_t wg_limit = wg ? wg_capacity : workgroups + workgroups / 3 + 2;
+  int64_t max_load = 0;  // largest workgroup load of the last walk, in cost units
+  auto walk = [&](int64_t share_units, int64_t& items, int64_t& wgs) -> int {
+    items = 0;
+    wgs = 0;
+    max_load = 0;
+    int64_t r = 0, pos = 0;  // request, tile within it
+    while (r < batch) {
+      if (wgs >= wg_limit) return 1;
+      if (wg) wg[wgs] = static_cast<int32_t>(items);
+      ++wgs;
+      int64_t budget = share_units;
+      while (r < batch) {
+        const int64_t tiles = (lengths[r] + tile - 1) / tile;
+        const int64_t take = std::min({budget / kUnit, tiles - pos, max_item_tiles});
+        if (take <= 0 && tiles > 0) break;
+        if (items >= capacity) return 2;
+        work[4 * items + 0] = static_cast<int32_t>(r);
+        work[4 * items + 1] = static_cast<int32_t>(pos * tile);
+        work[4 * items + 2] =
+            static_cast<int32_t>(std::min<int64_t>((pos + take) * tile, lengths[r]));
+        ++items;
+        budget -= take * kUnit + kItemCost;
+        pos += take;
+        if (pos == tiles) {
+          ++r;
+          pos = 0;
+        }
       }
-      if (budget < kSliver) break;  // no sliver at the share end
+      max_load = std::max(max_load, share_units - budget);
+    }
+    return 0;
+  };
+  // A share this large puts every request in one workgroup's items, so the search ends.
+  const int64_t everything = total * kUnit + (batch + 1) * kItemCost + kUnit;
+  int64_t items = 0, wgs = 0;
+  for (;;) {
+    const int status = walk(share, items, wgs);
+    if (status == 2 || (status == 1 && share >= everything)) return -1;
+    if (status == 0 && (wgs <= workgroups || share >= everything)) break;
+    const int64_t over = status == 0 ? wgs - workgroups : workgroups / 8 + 1;
+    share = std::min(everything, share + std::max<int64_t>(1, share * over / (4 * workgroups)));
+  }
+  // The alternative of whole requests, one item each, placed longest first on the least
+  // loaded workgroup: no partials and no merge launch, which outweighs a somewhat longer
+  // longest workgroup (batches of nearly equal requests, such as config 5's decode
+  // steps: 230.7 us per launch whole against 236.5 balanced and 244.4 with the item cost
+  // at 6/8 of a tile).
+  const bool split = items > batch;
+  bool whole = split && wg_limit >= std::min(batch, workgroups);
+  for (int64_t r = 0; whole && r < batch; ++r) whole = lengths[r] <= max_item;
+  if (whole) {
+    const int64_t bins = std::min(batch, workgroups);
+    std::vector<int64_t> order(batch);
+    for (int64_t r = 0; r < batch; ++r) order[r] = r;
+    std::stable_sort(order.begin(), order.end(), [&](int64_t x, int64_t y) {
+      return lengths[x] > lengths[y];
+    });
+    // Min-heap of (load, bin).
+    std::vector<std::pair<int64_t, int64_t>> heap;
+    heap.reserve(bins);
+    for (int64_t b = 0; b < bins; ++b) heap.emplace_back(0, b);
+    std::vector<int64_t> bin_of(batch);
+    int64_t whole_load = 0;
+    for (const int64_t r : order) {
+      std::pop_heap(heap.begin(), heap.end(), std::greater<>());
+      auto& top = heap.back();
+      top.first += (lengths[r] + tile - 1) / tile * kUnit + kItemCost;
+      whole_load = std::max(whole_load, top.first);
+      bin_of[r] = top.second;
+      std::push_heap(heap.begin(), heap.end(), std::greater<>());
+    }
+    if (whole_load <= max_load + kMergeCost && batch <= capacity) {
+      // Items grouped by bin (requests in their original order within a bin).
+      std::vector<int64_t> first(bins + 1, 0);
+      for (int64_t r = 0; r < batch; ++r) ++first[bin_of[r] + 1];
+      for (int64_t b = 0; b < bins; ++b) first[b + 1] += first[b];
+      std::vector<int64_t> next(first.begin(), first.end() - 1);
+      for (int64_t r = 0; r < batch; ++r) {
+        const int64_t i = next[bin_of[r]]++;
+        work[4 * i + 0] = static_cast<int32_t>(r);
+        work[4 * i + 1] = 0;
+        work[4 * i + 2] = lengths[r];
+      }
+      if (wg)
+        for (int64_t b = 0; b < bins; ++b) wg[b] = static_cast<int32_t>(first[b]);
+      items = batch;
+      wgs = bins;
+      share = whole_load;
     }
   }
   if (wg) wg[wgs] = static_cast<int32_t>(items);
@@ -298,7 +398,7 @@ int64_t schedule(const int32_t* lengths, int64_t batch, int64_t workgroups, int6
     if (n > 1) partials += n;
     i += n;
   }
-  *share_out = share;
+  *share_out = share / kUnit * tile;
   if (wgs_out) *wgs_out = wgs;
   return items;
 }
@@ -320,6 +420,26 @@ __global__ __launch_bounds__(256) void pack_page_metadata(const int32_t* __restr
   for (int c = threadIdx.x; c < pages; c += blockDim.x) indices[begin + c] = src[c];
 }
 
+// Slots of the first tile of each workgroup's first item, into its start record (the
+// planner wrote the rest of the record; `indices` is pack_page_metadata's output).
+// One thread per (workgroup, token of the tile); tokens past the item are clamped to
+// its last, as the decode kernels clamp them.
+__global__ __launch_bounds__(256) void pack_start_slots(int32_t* __restrict__ recs,
+                                                        const int32_t* __restrict__ indices,
+                                                        int32_t wgs, int32_t page_size) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int w = i / kDmaTile, j = i % kDmaTile;
+  if (w >= wgs) return;
+  int32_t* r = recs + kWgRec * w;
+  if (r[0] >= r[1]) return;
+  const int beg = r[3], end = r[4];
+  const int tok = min(beg + j, end - 1);
+  const int e = indices[r[6] + tok / page_size - beg / page_size];
+  r[kWgRecSlots + j] = static_cast<int32_t>(static_cast<uint32_t>(e) *
+                                                static_cast<uint32_t>(page_size) +
+                                            static_cast<uint32_t>(tok % page_size));
+}
+
 // ---------------------------------------------------------------------------
 // Decode kernel.
 // ---------------------------------------------------------------------------
@@ -331,7 +451,7 @@ struct DecodeArgs {
   uint16_t* out;
   int64_t out_stride_n, out_stride_h;
   const int32_t* ints;  // workspace (num_items, indptr, work, merge)
-  int32_t o_indptr, o_work, o_merge, o_wg;
+  int32_t o_indptr, o_work, o_merge, o_wg, o_wgrec;
   const int32_t* indices;
   float* partial_o;
   float* partial_lse;
@@ -555,6 +675,40 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
 }  // item loop
 }
 
+// An item's page entries [0, n) -> LDS by direct copies (4 bytes per lane; lanes past
+// n read entry n - 1, so every read stays inside the item's pages; the writes past n
+// stay inside the entries array, whose size is a multiple of 64).
+template <int W>
+__device__ __forceinline__ void stage_entries(const int32_t* pages, int n, uint32_t lds,
+                                              int wave, int lane) {
+  for (int base = wave * 64; base < n; base += W * 64)
+    copy_dword_to_lds(pages + min(base + lane, n - 1), lds + base * 4);
+}
+
+// Start of a work item: its request, token range, partial slot and the index of its
+// first page entry in `indices`.
+struct ItemStart {
+  int req, beg, end, pslot, page_base;
+};
+
+__device__ __forceinline__ ItemStart item_start(const DecodeArgs& a, int item) {
+  const int4 wi = reinterpret_cast<const int4*>(a.ints + a.o_work)[item];
+  return {wi.x, wi.y, wi.z, wi.w, a.ints[a.o_indptr + wi.x] + wi.y / a.page_size};
+}
+
+// A workgroup's start record (written by the planner and pack_start_slots), read with
+// uniform loads from the constant address space so they become scalar loads that do
+// not depend on each other: the first tile's copies need one round trip.
+struct WgRecord {
+  const __attribute__((address_space(4))) int32_t* p;
+  __device__ WgRecord(const DecodeArgs& a, int wg)
+      : p((const __attribute__((address_space(4))) int32_t*)(a.ints + a.o_wgrec) + kWgRec * wg) {}
+  __device__ int item_begin() const { return p[0]; }
+  __device__ int item_end() const { return p[1]; }
+  __device__ ItemStart start() const { return {p[2], p[3], p[4], p[5], p[6]}; }
+  __device__ uint32_t slot(int i) const { return static_cast<uint32_t>(p[kWgRecSlots + i]); }
+};
+
 // ---------------------------------------------------------------------------
 // Decode with direct-to-LDS staging. One workgroup of W waves (one per kv head of
 // its head slice) per CU; the grid is the balanced split-KV schedule, so every
@@ -585,47 +739,67 @@ __global__ __launch_bounds__(64 * W, 1) void decode_dma_kernel(DecodeArgs a) {
   const int h = blockIdx.y * W + wave;  // kv head
   const int wg = blockIdx.x;
   if (wg >= a.ints[0]) return;  // graph plans launch a fixed capacity
-  if (a.num_kv_heads < 0) lds[threadIdx.x] = 0;  // the copies are invisible to the compiler
+  if (a.num_kv_heads < 0) {  // the copies are invisible to the compiler
+    lds[threadIdx.x] = 0;
+    entries[threadIdx.x] = 0;
+  }
   const uint32_t lds_base = lds_address(lds);
+  const uint32_t entries_lds = lds_address(entries);
   const uint32_t row_elems = static_cast<uint32_t>(a.num_kv_heads) * kHeadDim;
   const uint16_t* kslice = a.k_cache + blockIdx.y * W * kHeadDim;
   const uint16_t* vslice = a.v_cache + blockIdx.y * W * kHeadDim;
-  const int item_end = a.ints[a.o_wg + wg + 1];
+  const WgRecord rec(a, wg);
+  const int item_begin = rec.item_begin(), item_end = rec.item_end();
 
-  for (int item = a.ints[a.o_wg + wg]; item < item_end; ++item) {
-    const int4 wi = reinterpret_cast<const int4*>(a.ints + a.o_work)[item];
-    const int req = wi.x, beg = wi.y, end = wi.z, pslot = wi.w;
-    // Page entries of tokens [beg, end) -> LDS (the previous item's readers are done).
+  for (int item = item_begin; item < item_end; ++item) {
+    // The workgroup's first item comes from its start record, whose slots let the first
+    // tile's copies issue before the page entries are staged.
+    const bool first = item == item_begin;
+    const ItemStart is = first ? rec.start() : item_start(a, item);
+    const int req = is.req, beg = is.beg, end = is.end, pslot = is.pslot;
     const int first_page = beg / a.page_size;
     const int n_entries = (end - 1) / a.page_size - first_page + 1;
-    const int32_t* pages = a.indices + a.ints[a.o_indptr + req] + first_page;
-    __syncthreads();
-    for (int i = threadIdx.x; i < n_entries; i += blockDim.x) entries[i] = pages[i];
-    uint4 qv[G];
-#pragma unroll
-    for (int gi = 0; gi < G; ++gi)
-      qv[gi] = ld128(a.q + req * a.q_stride_n + (h * G + gi) * a.q_stride_h + sub * 8);
-    wait_vmem_loads();
-    __syncthreads();
-
+    const int32_t* pages = a.indices + is.page_base;
     const int n_tiles = (end - beg + T - 1) / T;
     // Copy c of a tile: half c / (kCopies / 2) (K, V), token (c % (kCopies / 2)) * 1024 /
     // kRow of the tile, byte (c * 1024) % kRow of its row; the token is wave-uniform.
-    auto issue = [&](int t, int stage) {
+    // Tile 0 of the first item reads its slots from the start record, every other tile
+    // from the page entries staged in LDS.
+    auto issue = [&](int t, int stage, bool from_record) {
 #pragma unroll
       for (int j = 0; j < kPerWave; ++j) {
         const int c = wave * kPerWave + j;
         const int half = c / (kCopies / 2);
         const int r = c % (kCopies / 2);
         const int tok = min(beg + t * T + (r * 1024) / kRow, end - 1);
-        const int e = entries[tok / a.page_size - first_page];
-        const uint32_t slot = static_cast<uint32_t>(e) * static_cast<uint32_t>(a.page_size) +
-                              static_cast<uint32_t>(tok % a.page_size);
+        uint32_t slot;
+        if (from_record) {
+          slot = rec.slot(tok - beg);
+        } else {
+          const int e = entries[tok / a.page_size - first_page];
+          slot = static_cast<uint32_t>(e) * static_cast<uint32_t>(a.page_size) +
+                 static_cast<uint32_t>(tok % a.page_size);
+        }
         const uint16_t* src = (half ? vslice : kslice) + static_cast<uint64_t>(slot) * row_elems +
                               ((r * 1024) % kRow) / 2 + lane * 8;
         copy_to_lds(src, lds_base + stage * kStage + half * kHalf + r * 1024);
       }
     };
+    // Page entries of tokens [beg, end) -> LDS (the previous item's readers are done),
+    // then the query rows. The first item's tile 0 issues right behind them; the loop's
+    // first wait (vmcnt 0) covers entries, queries and that tile, and its barrier makes
+    // the entries visible before tile 1 is issued.
+    if (!first) __syncthreads();
+    stage_entries<W>(pages, n_entries, entries_lds, wave, lane);
+    uint4 qv[G];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi)
+      qv[gi] = ld128(a.q + req * a.q_stride_n + (h * G + gi) * a.q_stride_h + sub * 8);
+    if (first) issue(0, 0, true);  // nothing has used the ring yet
+    if (!first || S > 2) {
+      wait_vmem_loads();
+      __syncthreads();
+    }
 
     float m[G], l[G], o[G][8];
 #pragma unroll
@@ -635,13 +809,12 @@ __global__ __launch_bounds__(64 * W, 1) void decode_dma_kernel(DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[gi][i] = 0.f;
     }
-#pragma unroll
-    for (int st = 0; st < S - 1; ++st)
-      if (st < n_tiles) issue(st, st);
+    for (int st = first ? 1 : 0; st < S - 1; ++st)
+      if (st < n_tiles) issue(st, st, false);
     for (int t = 0; t < n_tiles; ++t) {
       wait_tiles_ahead<kPerWave, S - 2>(min(S - 2, n_tiles - 1 - t));
       __syncthreads();
-      if (t + S - 1 < n_tiles) issue(t + S - 1, (t + S - 1) % S);
+      if (t + S - 1 < n_tiles) issue(t + S - 1, (t + S - 1) % S, false);
       const uint8_t* sb = lds + (t % S) * kStage + wave * 256 + sub * 16;
       uint4 kr[U], vr[U];
       bool ok[U];
@@ -759,24 +932,59 @@ __global__ __launch_bounds__(64 * W, 1) void decode_mma_kernel(DecodeArgs a) {
   const int h = blockIdx.y * W + wave;  // kv head
   const int wg = blockIdx.x;
   if (wg >= a.ints[0]) return;  // graph plans launch a fixed capacity
-  if (a.num_kv_heads < 0) lds[threadIdx.x] = 0;  // the copies are invisible to the compiler
+  if (a.num_kv_heads < 0) {  // the copies are invisible to the compiler
+    lds[threadIdx.x] = 0;
+    entries[threadIdx.x] = 0;
+  }
   const uint32_t lds_base = lds_address(lds);
+  const uint32_t entries_lds = lds_address(entries);
   const uint32_t row_elems = static_cast<uint32_t>(a.num_kv_heads) * kHeadDim;
   const uint16_t* kslice = a.k_cache + blockIdx.y * W * kHeadDim;
   const uint16_t* vslice = a.v_cache + blockIdx.y * W * kHeadDim;
-  const int item_end = a.ints[a.o_wg + wg + 1];
+  const WgRecord rec(a, wg);
+  const int item_begin = rec.item_begin(), item_end = rec.item_end();
 
   // Read offsets within a stage for this wave's head (token-independent parts).
   const int head_off = wave * 256;
 
-  for (int item = a.ints[a.o_wg + wg]; item < item_end; ++item) {
-    const int4 wi = reinterpret_cast<const int4*>(a.ints + a.o_work)[item];
-    const int req = wi.x, beg = wi.y, end = wi.z, pslot = wi.w;
+  for (int item = item_begin; item < item_end; ++item) {
+    // The first item comes from the start record (see decode_dma_kernel).
+    const bool first = item == item_begin;
+    const ItemStart is = first ? rec.start() : item_start(a, item);
+    const int req = is.req, beg = is.beg, end = is.end, pslot = is.pslot;
     const int first_page = beg / a.page_size;
     const int n_entries = (end - 1) / a.page_size - first_page + 1;
-    const int32_t* pages = a.indices + a.ints[a.o_indptr + req] + first_page;
-    __syncthreads();
-    for (int i = threadIdx.x; i < n_entries; i += blockDim.x) entries[i] = pages[i];
+    const int32_t* pages = a.indices + is.page_base;
+    const int n_tiles = (end - beg + T - 1) / T;
+    // Copy c of a tile: half c / (kCopies / 2) (K, V), token (c % (kCopies / 2)) * 1024 /
+    // kRow of the tile, byte (c * 1024) % kRow of its row; the token is wave-uniform.
+    // Lane i fetches the chunk that belongs at position i: chunk (i ^ (token & 15)) of
+    // the same head. Tile 0 of the first item reads its slots from the start record.
+    auto issue = [&](int t, int stage, bool from_record) {
+#pragma unroll
+      for (int j = 0; j < kPerWave; ++j) {
+        const int c = wave * kPerWave + j;
+        const int half = c / (kCopies / 2);
+        const int r = c % (kCopies / 2);
+        const int tile_tok = (r * 1024) / kRow;
+        const int tok = min(beg + t * T + tile_tok, end - 1);
+        uint32_t slot;
+        if (from_record) {
+          slot = rec.slot(tok - beg);
+        } else {
+          const int e = entries[tok / a.page_size - first_page];
+          slot = static_cast<uint32_t>(e) * static_cast<uint32_t>(a.page_size) +
+                 static_cast<uint32_t>(tok % a.page_size);
+        }
+        const int chunk = ((r * 1024) % kRow) / 16 + lane;  // position within the row
+        const int src_chunk = (chunk & ~15) | ((chunk & 15) ^ (tile_tok & 15));
+        const uint16_t* src =
+            (half ? vslice : kslice) + static_cast<uint64_t>(slot) * row_elems + src_chunk * 8;
+        copy_to_lds(src, lds_base + stage * kStage + half * kHalf + r * 1024);
+      }
+    };
+    if (!first) __syncthreads();
+    stage_entries<W>(pages, n_entries, entries_lds, wave, lane);
     // Q^T as the B operand: lane holds q head (h G + col) dims 32 kk + 8 quad .. + 8;
     // columns past the group are zero.
     uint4 qb[4];
@@ -786,45 +994,24 @@ __global__ __launch_bounds__(64 * W, 1) void decode_mma_kernel(DecodeArgs a) {
                                32 * kk + 8 * quad)
                        : make_uint4(0, 0, 0, 0);
     }
-    wait_vmem_loads();
-    __syncthreads();
+    if (first) issue(0, 0, true);  // nothing has used the ring yet
+    if (!first || S > 2) {
+      wait_vmem_loads();
+      __syncthreads();
+    }
 
-    const int n_tiles = (end - beg + T - 1) / T;
-    // Copy c of a tile: half c / (kCopies / 2) (K, V), token (c % (kCopies / 2)) * 1024 /
-    // kRow of the tile, byte (c * 1024) % kRow of its row; the token is wave-uniform.
-    // Lane i fetches the chunk that belongs at position i: chunk (i ^ (token & 15)) of
-    // the same head.
-    auto issue = [&](int t, int stage) {
-#pragma unroll
-      for (int j = 0; j < kPerWave; ++j) {
-        const int c = wave * kPerWave + j;
-        const int half = c / (kCopies / 2);
-        const int r = c % (kCopies / 2);
-        const int tile_tok = (r * 1024) / kRow;
-        const int tok = min(beg + t * T + tile_tok, end - 1);
-        const int e = entries[tok / a.page_size - first_page];
-        const uint32_t slot = static_cast<uint32_t>(e) * static_cast<uint32_t>(a.page_size) +
-                              static_cast<uint32_t>(tok % a.page_size);
-        const int chunk = ((r * 1024) % kRow) / 16 + lane;  // position within the row
-        const int src_chunk = (chunk & ~15) | ((chunk & 15) ^ (tile_tok & 15));
-        const uint16_t* src =
-            (half ? vslice : kslice) + static_cast<uint64_t>(slot) * row_elems + src_chunk * 8;
-        copy_to_lds(src, lds_base + stage * kStage + half * kHalf + r * 1024);
-      }
-    };
 
     mma_floatx4 o[8];
 #pragma unroll
     for (int b = 0; b < 8; ++b) o[b] = mma_floatx4{0.f, 0.f, 0.f, 0.f};
     float m = -1e30f, l = 0.f;  // of column `col`; m is the same in the 4 lane groups
 
-#pragma unroll
-    for (int st = 0; st < S - 1; ++st)
-      if (st < n_tiles) issue(st, st);
+    for (int st = first ? 1 : 0; st < S - 1; ++st)
+      if (st < n_tiles) issue(st, st, false);
     for (int t = 0; t < n_tiles; ++t) {
       wait_tiles_ahead<kPerWave, S - 2>(min(S - 2, n_tiles - 1 - t));
       __syncthreads();
-      if (t + S - 1 < n_tiles) issue(t + S - 1, (t + S - 1) % S);
+      if (t + S - 1 < n_tiles) issue(t + S - 1, (t + S - 1) % S, false);
       const uint8_t* kb = lds + (t % S) * kStage + head_off;
       const uint8_t* vb = kb + kHalf;
       // S = K Q^T: lane reads token `col`, chunk 4 kk + quad (swizzled).
@@ -1042,7 +1229,8 @@ extern "C" int64_t mi355x_decode_schedule(const int32_t* lengths, int64_t batch,
     if (lengths[r] <= 0) return -1;
   // The host-only view: page size 1 and no cap on item length.
   const LaunchShape shape = launch_shape(cus, num_kv_heads, 1);
-  return schedule(lengths, batch, shape.workgroups, std::numeric_limits<int32_t>::max(), work,
+  return schedule(lengths, batch, shape.workgroups, std::numeric_limits<int32_t>::max(),
+                  shape.tile, work,
                   work_capacity, merge, chunk_tokens);
 }
 
@@ -1184,7 +1372,7 @@ extern "C" void* mi355x_decode_prepare(void* existing, const int32_t* block_tabl
                                       (plan->host_lengths[r] + page_size - 1) / page_size);
     int64_t chunk = 0, wgs = 0;
     const int64_t items = schedule(plan->host_lengths.data(), batch, shape.workgroups,
-                                   shape.max_item, host + layout.o_work, items_cap,
+                                   shape.max_item, shape.tile, host + layout.o_work, items_cap,
                                    host + layout.o_merge, &chunk, host + layout.o_wg, wg_cap, &wgs);
     if (items < 0) {
       set_error("decode work list exceeds its capacity");
@@ -1192,6 +1380,22 @@ extern "C" void* mi355x_decode_prepare(void* existing, const int32_t* block_tabl
     }
     host[0] = static_cast<int32_t>(wgs);
     host[1] = static_cast<int32_t>(items);
+    // Start records: the first item of each workgroup and the page-entry index of its
+    // first token (the slots are filled on the device once `indices` is packed).
+    for (int64_t w = 0; w < wgs; ++w) {
+      int32_t* rec = host + layout.o_wgrec + kWgRec * w;
+      const int32_t* first = host + layout.o_wg;
+      rec[0] = first[w];
+      rec[1] = first[w + 1];
+      if (rec[0] < rec[1]) {
+        const int32_t* wi = host + layout.o_work + 4 * static_cast<int64_t>(rec[0]);
+        rec[2] = wi[0];
+        rec[3] = wi[1];
+        rec[4] = wi[2];
+        rec[5] = wi[3];
+        rec[6] = indptr[wi[0]] + wi[1] / static_cast<int32_t>(page_size);
+      }
+    }
     st = hipMemcpyAsync(plan->ints.ptr, host, int_bytes, hipMemcpyHostToDevice, s);
     if (st != hipSuccess) {
       hip_error(st, "decode metadata upload");
@@ -1204,6 +1408,17 @@ extern "C" void* mi355x_decode_prepare(void* existing, const int32_t* block_tabl
     if (const char* err = launch_status("pack_page_metadata")) {
       (void)err;
       return nullptr;
+    }
+    if (wgs > 0) {
+      const int64_t threads = wgs * kDmaTile;
+      pack_start_slots<<<dim3(static_cast<uint32_t>((threads + 255) / 256)), dim3(256), 0, s>>>(
+          static_cast<int32_t*>(plan->ints.ptr) + layout.o_wgrec,
+          static_cast<const int32_t*>(plan->indices.ptr), static_cast<int32_t>(wgs),
+          static_cast<int32_t>(page_size));
+      if (const char* err = launch_status("pack_start_slots")) {
+        (void)err;
+        return nullptr;
+      }
     }
     st = hipEventRecord(plan->upload_done, s);
     if (st != hipSuccess) {
@@ -1300,6 +1515,7 @@ extern "C" const char* mi355x_decode_run(const void* plan_ptr, const void* q, in
   a.o_work = static_cast<int32_t>(p.layout.o_work);
   a.o_merge = static_cast<int32_t>(p.layout.o_merge);
   a.o_wg = static_cast<int32_t>(p.layout.o_wg);
+  a.o_wgrec = static_cast<int32_t>(p.layout.o_wgrec);
   a.indices = static_cast<const int32_t*>(p.indices.ptr);
   a.partial_o = static_cast<float*>(p.partial_o.ptr);
   a.partial_lse = static_cast<float*>(p.partial_lse.ptr);

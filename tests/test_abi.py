@@ -74,6 +74,22 @@ def test_decode_schedule_config2_shape(native):
     assert chunk >= 128
 
 
+def test_decode_schedule_cuts_on_tiles(native):
+    """Shares are counted in the decode kernels' 16-token tiles plus a per-item cost: cuts
+    fall on tile boundaries, and a batch of nearly equal requests (the config-5 decode
+    shape) is not cut at all."""
+    rng = np.random.default_rng(2)
+    lengths = rng.integers(512, 4097, size=64).tolist()
+    n, work, merge, chunk, cap = _schedule(native, lengths)
+    items = np.array(work).reshape(-1, 4)
+    assert (items[:, 1] % 16 == 0).all()
+    assert n <= 256 + len(lengths)  # one cut per share boundary at most
+    lengths = (1280 + rng.integers(-32, 33, size=256)).tolist()
+    n, work, merge, chunk, cap = _schedule(native, lengths)
+    oplan.check_work_list(work, merge, lengths)
+    assert n == 256 and all(c == 1 for c in merge[1::2])
+
+
 def test_decode_schedule_rejects_bad_input(native):
     lib = native.lib()
     lens = (ctypes.c_int32 * 2)(5, 0)
