@@ -32,6 +32,7 @@
 // slices straight into registers.
 #include <algorithm>
 #include <functional>
+#include <type_traits>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -285,8 +286,13 @@ int64_t schedule(const int32_t* lengths, int64_t batch, int64_t workgroups, int6
   // decode launch takes 4.3 us longer with six requests split than with none).
   constexpr int64_t kMergeCost = 16;
   const int64_t max_item_tiles = std::max<int64_t>(1, max_item / tile);
+  // Tiles per request, computed once (the walks below run a dozen times per plan).
+  std::vector<int32_t> tiles_of(batch);
   int64_t total = 0;
-  for (int64_t r = 0; r < batch; ++r) total += (lengths[r] + tile - 1) / tile;
+  for (int64_t r = 0; r < batch; ++r) {
+    tiles_of[r] = static_cast<int32_t>((lengths[r] + tile - 1) / tile);
+    total += tiles_of[r];
+  }
   const int64_t min_share = std::max<int64_t>(1, kMinShareTokens / tile) * kUnit;
   // Smallest share (cost units) whose walk needs at most `workgroups` workgroups: start
   // from the tile-only bound and add item costs until the walk fits.
@@ -295,25 +301,30 @@ int64_t schedule(const int32_t* lengths, int64_t batch, int64_t workgroups, int6
   // workgroups, 2 when the item capacity is too small.
   const int64_t wg_limit = wg ? wg_capacity : workgroups + workgroups / 3 + 2;
   int64_t max_load = 0;  // largest workgroup load of the last walk, in cost units
-  auto walk = [&](int64_t share_units, int64_t& items, int64_t& wgs) -> int {
+  // `write` (std::true_type / std::false_type): fill the work list and workgroup starts,
+  // or only count (the search below).
+  auto walk = [&](int64_t share_units, int64_t& items, int64_t& wgs, auto write) -> int {
+    constexpr bool kWrite = decltype(write)::value;
     items = 0;
     wgs = 0;
     max_load = 0;
     int64_t r = 0, pos = 0;  // request, tile within it
     while (r < batch) {
       if (wgs >= wg_limit) return 1;
-      if (wg) wg[wgs] = static_cast<int32_t>(items);
+      if (kWrite && wg) wg[wgs] = static_cast<int32_t>(items);
       ++wgs;
       int64_t budget = share_units;
       while (r < batch) {
-        const int64_t tiles = (lengths[r] + tile - 1) / tile;
-        const int64_t take = std::min({budget / kUnit, tiles - pos, max_item_tiles});
+        const int64_t tiles = tiles_of[r];
+        const int64_t take = std::min(std::min(budget / kUnit, tiles - pos), max_item_tiles);
         if (take <= 0 && tiles > 0) break;
         if (items >= capacity) return 2;
-        work[4 * items + 0] = static_cast<int32_t>(r);
-        work[4 * items + 1] = static_cast<int32_t>(pos * tile);
-        work[4 * items + 2] =
-            static_cast<int32_t>(std::min<int64_t>((pos + take) * tile, lengths[r]));
+        if constexpr (kWrite) {
+          work[4 * items + 0] = static_cast<int32_t>(r);
+          work[4 * items + 1] = static_cast<int32_t>(pos * tile);
+          work[4 * items + 2] =
+              static_cast<int32_t>(std::min<int64_t>((pos + take) * tile, lengths[r]));
+        }
         ++items;
         budget -= take * kUnit + kItemCost;
         pos += take;
@@ -328,14 +339,39 @@ int64_t schedule(const int32_t* lengths, int64_t batch, int64_t workgroups, int6
   };
   // A share this large puts every request in one workgroup's items, so the search ends.
   const int64_t everything = total * kUnit + (batch + 1) * kItemCost + kUnit;
+  // The workgroup count of a walk does not grow with the share: find the smallest share
+  // that fits by an exponential then a binary search (about a dozen walks).
   int64_t items = 0, wgs = 0;
-  for (;;) {
-    const int status = walk(share, items, wgs);
-    if (status == 2 || (status == 1 && share >= everything)) return -1;
-    if (status == 0 && (wgs <= workgroups || share >= everything)) break;
-    const int64_t over = status == 0 ? wgs - workgroups : workgroups / 8 + 1;
-    share = std::min(everything, share + std::max<int64_t>(1, share * over / (4 * workgroups)));
+  auto fits = [&](int64_t share_units, int& status) {
+    status = walk(share_units, items, wgs, std::false_type{});
+    return status == 0 && (wgs <= workgroups || share_units >= everything);
+  };
+  int status = 0;
+  if (!fits(share, status)) {
+    if (status == 2) return -1;
+    // First guess: every request and every workgroup boundary adds one item.
+    int64_t lo = share, hi = share;
+    int64_t step = std::max<int64_t>(
+        kUnit, ((batch + workgroups) * kItemCost + workgroups - 1) / workgroups);
+    for (;;) {  // lo does not fit; find a hi that does
+      hi = std::min(everything, lo + step);
+      if (fits(hi, status)) break;
+      if (status == 2 || hi >= everything) return -1;
+      lo = hi;
+      step *= 2;
+    }
+    while (hi - lo > 1) {
+      const int64_t mid = lo + (hi - lo) / 2;
+      if (fits(mid, status)) {
+        hi = mid;
+      } else {
+        if (status == 2) return -1;
+        lo = mid;
+      }
+    }
+    share = hi;
   }
+  if (walk(share, items, wgs, std::true_type{}) != 0) return -1;
   // The alternative of whole requests, one item each, placed longest first on the least
   // loaded workgroup: no partials and no merge launch, which outweighs a somewhat longer
   // longest workgroup (batches of nearly equal requests, such as config 5's decode
@@ -346,24 +382,30 @@ int64_t schedule(const int32_t* lengths, int64_t batch, int64_t workgroups, int6
   for (int64_t r = 0; whole && r < batch; ++r) whole = lengths[r] <= max_item;
   if (whole) {
     const int64_t bins = std::min(batch, workgroups);
-    std::vector<int64_t> order(batch);
-    for (int64_t r = 0; r < batch; ++r) order[r] = r;
-    std::stable_sort(order.begin(), order.end(), [&](int64_t x, int64_t y) {
-      return lengths[x] > lengths[y];
-    });
-    // Min-heap of (load, bin).
-    std::vector<std::pair<int64_t, int64_t>> heap;
-    heap.reserve(bins);
-    for (int64_t b = 0; b < bins; ++b) heap.emplace_back(0, b);
     std::vector<int64_t> bin_of(batch);
     int64_t whole_load = 0;
-    for (const int64_t r : order) {
-      std::pop_heap(heap.begin(), heap.end(), std::greater<>());
-      auto& top = heap.back();
-      top.first += (lengths[r] + tile - 1) / tile * kUnit + kItemCost;
-      whole_load = std::max(whole_load, top.first);
-      bin_of[r] = top.second;
-      std::push_heap(heap.begin(), heap.end(), std::greater<>());
+    if (batch <= workgroups) {  // a workgroup per request
+      for (int64_t r = 0; r < batch; ++r) {
+        bin_of[r] = r;
+        whole_load = std::max(whole_load, tiles_of[r] * kUnit + kItemCost);
+      }
+    } else {
+      std::vector<int64_t> order(batch);
+      for (int64_t r = 0; r < batch; ++r) order[r] = r;
+      std::stable_sort(order.begin(), order.end(),
+                       [&](int64_t x, int64_t y) { return tiles_of[x] > tiles_of[y]; });
+      // Min-heap of (load, bin).
+      std::vector<std::pair<int64_t, int64_t>> heap;
+      heap.reserve(bins);
+      for (int64_t b = 0; b < bins; ++b) heap.emplace_back(0, b);
+      for (const int64_t r : order) {
+        std::pop_heap(heap.begin(), heap.end(), std::greater<>());
+        auto& top = heap.back();
+        top.first += tiles_of[r] * kUnit + kItemCost;
+        whole_load = std::max(whole_load, top.first);
+        bin_of[r] = top.second;
+        std::push_heap(heap.begin(), heap.end(), std::greater<>());
+      }
     }
     if (whole_load <= max_load + kMergeCost && batch <= capacity) {
       // Items grouped by bin (requests in their original order within a bin).
@@ -411,8 +453,24 @@ __global__ __launch_bounds__(256) void pack_page_metadata(const int32_t* __restr
                                                           const int32_t* __restrict__ indptr,
                                                           int32_t* __restrict__ indices,
                                                           int32_t* __restrict__ last_len,
-                                                          int64_t stride, int32_t page_size) {
+                                                          int64_t stride, int32_t page_size,
+                                                          int32_t* __restrict__ recs,
+                                                          int32_t wgs, int32_t rows) {
   const int row = blockIdx.x;
+  // Workgroup `row`'s start record: the KV slots of its first item's first tile, read
+  // from the block table (tokens past the item clamp to its last, as the decode kernels
+  // clamp them). The planner wrote the rest of the record.
+  if (row < wgs && threadIdx.x < kDmaTile) {
+    int32_t* r = recs + kWgRec * row;
+    if (r[0] < r[1]) {
+      const int req = r[2], beg = r[3], end = r[4];
+      const int tok = min(beg + static_cast<int>(threadIdx.x), end - 1);
+      const uint32_t page = static_cast<uint32_t>(table[req * stride + tok / page_size]);
+      r[kWgRecSlots + threadIdx.x] = static_cast<int32_t>(
+          page * static_cast<uint32_t>(page_size) + static_cast<uint32_t>(tok % page_size));
+    }
+  }
+  if (row >= rows) return;
   const int begin = indptr[row];
   const int pages = indptr[row + 1] - begin;
   if (threadIdx.x == 0) last_len[row] = (lengths[row] - 1) % page_size + 1;
@@ -420,25 +478,6 @@ __global__ __launch_bounds__(256) void pack_page_metadata(const int32_t* __restr
   for (int c = threadIdx.x; c < pages; c += blockDim.x) indices[begin + c] = src[c];
 }
 
-// Slots of the first tile of each workgroup's first item, into its start record (the
-// planner wrote the rest of the record; `indices` is pack_page_metadata's output).
-// One thread per (workgroup, token of the tile); tokens past the item are clamped to
-// its last, as the decode kernels clamp them.
-__global__ __launch_bounds__(256) void pack_start_slots(int32_t* __restrict__ recs,
-                                                        const int32_t* __restrict__ indices,
-                                                        int32_t wgs, int32_t page_size) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  const int w = i / kDmaTile, j = i % kDmaTile;
-  if (w >= wgs) return;
-  int32_t* r = recs + kWgRec * w;
-  if (r[0] >= r[1]) return;
-  const int beg = r[3], end = r[4];
-  const int tok = min(beg + j, end - 1);
-  const int e = indices[r[6] + tok / page_size - beg / page_size];
-  r[kWgRecSlots + j] = static_cast<int32_t>(static_cast<uint32_t>(e) *
-                                                static_cast<uint32_t>(page_size) +
-                                            static_cast<uint32_t>(tok % page_size));
-}
 
 // ---------------------------------------------------------------------------
 // Decode kernel.
@@ -696,7 +735,7 @@ __device__ __forceinline__ ItemStart item_start(const DecodeArgs& a, int item) {
   return {wi.x, wi.y, wi.z, wi.w, a.ints[a.o_indptr + wi.x] + wi.y / a.page_size};
 }
 
-// A workgroup's start record (written by the planner and pack_start_slots), read with
+// A workgroup's start record (written by the planner and pack_page_metadata), read with
 // uniform loads from the constant address space so they become scalar loads that do
 // not depend on each other: the first tile's copies need one round trip.
 struct WgRecord {
@@ -1364,7 +1403,9 @@ extern "C" void* mi355x_decode_prepare(void* existing, const int32_t* block_tabl
       return nullptr;
     }
     int32_t* host = static_cast<int32_t*>(plan->staging.ptr);
-    std::memset(host, 0, int_bytes);
+    // Everything before the start records starts at zero; the records of the workgroups
+    // launched are written in full below (those past them are never read).
+    std::memset(host, 0, layout.o_wgrec * sizeof(int32_t));
     int32_t* indptr = host + layout.o_indptr;
     indptr[0] = 0;
     for (int64_t r = 0; r < batch; ++r)
@@ -1381,10 +1422,11 @@ extern "C" void* mi355x_decode_prepare(void* existing, const int32_t* block_tabl
     host[0] = static_cast<int32_t>(wgs);
     host[1] = static_cast<int32_t>(items);
     // Start records: the first item of each workgroup and the page-entry index of its
-    // first token (the slots are filled on the device once `indices` is packed).
+    // first token (pack_page_metadata fills the slots from the block table).
     for (int64_t w = 0; w < wgs; ++w) {
       int32_t* rec = host + layout.o_wgrec + kWgRec * w;
       const int32_t* first = host + layout.o_wg;
+      std::memset(rec, 0, kWgRecSlots * sizeof(int32_t));
       rec[0] = first[w];
       rec[1] = first[w + 1];
       if (rec[0] < rec[1]) {
@@ -1396,29 +1438,21 @@ extern "C" void* mi355x_decode_prepare(void* existing, const int32_t* block_tabl
         rec[6] = indptr[wi[0]] + wi[1] / static_cast<int32_t>(page_size);
       }
     }
-    st = hipMemcpyAsync(plan->ints.ptr, host, int_bytes, hipMemcpyHostToDevice, s);
+    const size_t upload_bytes = (layout.o_wgrec + kWgRec * wgs) * sizeof(int32_t);
+    st = hipMemcpyAsync(plan->ints.ptr, host, upload_bytes, hipMemcpyHostToDevice, s);
     if (st != hipSuccess) {
       hip_error(st, "decode metadata upload");
       return nullptr;
     }
-    pack_page_metadata<<<dim3(static_cast<uint32_t>(batch)), dim3(256), 0, s>>>(
+    pack_page_metadata<<<dim3(static_cast<uint32_t>(std::max(batch, wgs))), dim3(256), 0, s>>>(
         block_table, seq_lens, static_cast<const int32_t*>(plan->ints.ptr) + layout.o_indptr,
         static_cast<int32_t*>(plan->indices.ptr), static_cast<int32_t*>(plan->last_len.ptr),
-        table_stride, static_cast<int32_t>(page_size));
+        table_stride, static_cast<int32_t>(page_size),
+        static_cast<int32_t*>(plan->ints.ptr) + layout.o_wgrec, static_cast<int32_t>(wgs),
+        static_cast<int32_t>(batch));
     if (const char* err = launch_status("pack_page_metadata")) {
       (void)err;
       return nullptr;
-    }
-    if (wgs > 0) {
-      const int64_t threads = wgs * kDmaTile;
-      pack_start_slots<<<dim3(static_cast<uint32_t>((threads + 255) / 256)), dim3(256), 0, s>>>(
-          static_cast<int32_t*>(plan->ints.ptr) + layout.o_wgrec,
-          static_cast<const int32_t*>(plan->indices.ptr), static_cast<int32_t>(wgs),
-          static_cast<int32_t>(page_size));
-      if (const char* err = launch_status("pack_start_slots")) {
-        (void)err;
-        return nullptr;
-      }
     }
     st = hipEventRecord(plan->upload_done, s);
     if (st != hipSuccess) {
