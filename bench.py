@@ -159,7 +159,8 @@ def e2e_section(dev, args) -> dict:
                "wall_s": round(wall, 3), "output_tokens": out_tokens,
                "prefill_batches": eng.stats["prefill_batches"],
                "decode_steps": eng.stats["decode_steps"],
-               "graph_steps": eng.stats["graph_steps"], "checks": checks}
+               "graph_steps": eng.stats["graph_steps"], "ahead_steps": eng.stats["ahead_steps"],
+               "overlap_steps": eng.stats["overlap_steps"], "checks": checks}
         del eng
         torch.cuda.empty_cache()
         return out
@@ -313,15 +314,18 @@ def summarize_gaps(path: str, idle_s: float = 0.2) -> str:
     the one with eager decode. Host-side text processing only (no GPU)."""
     import csv
 
-    spans = []
+    spans, names = [], {}
     with open(path, newline="") as f:
         for r in csv.DictReader(f):
+            name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
             spans.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
-                          "decode_mma_kernel" in r["Kernel_Name"]))
+                          "decode_mma_kernel" in r["Kernel_Name"],
+                          names.setdefault(name[:48], len(names))))
     spans.sort()
+    label = {v: k for k, v in names.items()}
     stretches, cur = [], []
     for sp in spans:
-        if cur and sp[0] - max(e for _, e, _ in cur[-64:]) > idle_s * 1e9:
+        if cur and sp[0] - max(x[1] for x in cur[-64:]) > idle_s * 1e9:
             stretches.append(cur)
             cur = []
         cur.append(sp)
@@ -329,23 +333,35 @@ def summarize_gaps(path: str, idle_s: float = 0.2) -> str:
         stretches.append(cur)
     lines = [f"{'stretch':>7s} {'kernels':>8s} {'decode_attn':>11s} {'span_s':>8s} {'busy_s':>8s} "
              f"{'idle_%':>7s} {'gap_median_us':>13s} {'gap_mean_us':>11s}"]
+    by_prev = []
     for i, st in enumerate(stretches):
         if len(st) < 1000:
             continue
-        gaps, end = [], st[0][1]
+        gaps, end, last = [], st[0][1], st[0][3]
         busy = 0
-        for b, e, _ in st:
+        after = {}  # idle time by the kernel whose end it follows
+        for b, e, _, k in st:
             busy += e - b
-            if b > end:
-                gaps.append((b - end) / 1e3)
-            else:
-                gaps.append(0.0)
-            end = max(end, e)
+            gap = (b - end) / 1e3 if b > end else 0.0
+            gaps.append(gap)
+            if gap > 0:
+                t = after.setdefault(last, [0.0, 0])
+                t[0] += gap
+                t[1] += 1
+            if e >= end:
+                end, last = e, k
         gaps = sorted(gaps[1:])
         span = (end - st[0][0]) / 1e9
         lines.append(f"{i:7d} {len(st):8d} {sum(1 for x in st if x[2]):11d} {span:8.3f} "
                      f"{busy / 1e9:8.3f} {100 * (1 - busy / 1e9 / span):7.2f} "
                      f"{gaps[len(gaps) // 2]:13.2f} {sum(gaps) / len(gaps):11.2f}")
+        by_prev.append((i, span, after))
+    for i, span, after in by_prev:
+        lines.append(f"# stretch {i}: idle time by the kernel it follows (top 8)")
+        lines.append(f"{'kernel':50s} {'idle_ms':>9s} {'% span':>7s} {'gaps':>7s} {'mean_us':>8s}")
+        for k, (t, n) in sorted(after.items(), key=lambda kv: -kv[1][0])[:8]:
+            lines.append(f"{label[k]:50s} {t / 1e3:9.2f} {100 * t / 1e6 / span:7.2f} {n:7d} "
+                         f"{t / n:8.2f}")
     return "\n".join(lines)
 
 

@@ -20,7 +20,10 @@ Mirrors the parts of the reference engine that feed the attention hot path:
   size, pad rows pointing at the reserved page 0 (length 1, slot 0 skipped by the K/V store),
   and the attention plan re-made outside the graph before each replay
   (``DecodeGraphState.prepare_replay``);
-* sampling with a pinned asynchronous readback (``src/engine/sampling.rs:193-237``).
+* sampling with a pinned asynchronous readback (``src/engine/sampling.rs:193-237``);
+* the CPU/GPU overlap of consecutive decode steps (``scheduler.rs:935-1000`` step_overlap):
+  the next graph step is launched with its input tokens copied on the device from this step's
+  sampling output, before the host reads them (``Engine._launch_ahead``).
 """
 from __future__ import annotations
 
@@ -48,6 +51,11 @@ class EngineConfig:
     num_pages: int | None = None           # default: every running request at max_seq_len
     graph_batch_sizes: tuple[int, ...] | None = None  # default 1, 2, 4, 8, 16, 24, ... <= max_running_req
     use_graphs: bool = True
+    # Launch the next graph decode step before this step's tokens reach the host, feeding them
+    # on the device (the reference's CPU/GPU overlap mode, ``scheduler.rs:935-1000``); only
+    # when the next step decodes exactly this step's rows (no prefill waiting, no row ending by
+    # length). False: the serial step of ``scheduler.rs:225-271`` every time.
+    overlap_decode: bool = True
     seed: int = 0
 
 
@@ -140,6 +148,15 @@ class _DecodeGraph:
 
 
 @dataclass
+class _InFlight:
+    """A graph decode step launched before the previous step's tokens reached the host: its
+    rows (the previous step's, in order) and the graph whose logits it fills."""
+
+    rows: list
+    graph: _DecodeGraph
+
+
+@dataclass
 class _Ahead:
     """A decode step staged one step early: its rows, their lengths, the graph bucket and the
     staged words (the input-token run still to be written once the tokens are known)."""
@@ -149,6 +166,10 @@ class _Ahead:
     graph: _DecodeGraph
     host: np.ndarray
     lens: np.ndarray
+
+    def same_rows(self, rows: list) -> bool:
+        """Staged for exactly these rows, in this order (none of them ends by length)."""
+        return len(rows) == len(self.uids) and all(r.uid == u for r, u in zip(rows, self.uids))
 
     def matches(self, rows: list, graph: _DecodeGraph) -> bool:
         """The staged step is the one to run: same graph, same rows in the same order, each
@@ -182,10 +203,11 @@ class Engine:
         self._staging = torch.empty(0, dtype=torch.int64, pin_memory=True)
         self._staging_copy: torch.cuda.Event | None = None
         self._ahead: _Ahead | None = None           # next decode step, staged while this one runs
+        self._inflight: _InFlight | None = None     # next decode step, already launched
         self._pending_rows: list[Request] | None = None
         self.graphs: dict[int, _DecodeGraph] = {}
         self.stats = {"prefill_batches": 0, "decode_steps": 0, "graph_steps": 0,
-                      "ahead_steps": 0}
+                      "ahead_steps": 0, "overlap_steps": 0}
         if cfg.use_graphs:
             self.capture_graphs()
 
@@ -368,11 +390,30 @@ class Engine:
         host, lens = self._stage_replay(graph, self.tables.prepare(reqs))
         self._ahead = _Ahead([r.uid for r in nxt], lengths, graph, host, lens)
 
+    def _launch_ahead(self, pending, rows: list[Request]) -> _InFlight | None:
+        """Launch the staged step now when it decodes exactly this step's rows: its words go
+        to the graph inputs with the input-token run overwritten on the device by this step's
+        sampled ids (the -1 of an invalid row clamped to 0; that row raises at its commit and
+        the launched step is dropped), then the re-plan and the replay. The host reads this
+        step's tokens afterwards, while the next step runs."""
+        ahead = self._ahead
+        if ahead is None or not self.cfg.overlap_decode or not ahead.same_rows(rows):
+            return None
+        self._ahead = None
+        g, n = ahead.graph, len(rows)
+        self._send(ahead.host.size, g.block)
+        torch.clamp(pending.ids, min=0, out=g.input_ids[:n])
+        g.state.prepare_replay(DecodeHostMetadata(ahead.lens))
+        g.graph.replay()
+        return _InFlight(rows, g)
+
     def _sample_and_commit(self, logits: torch.Tensor, rows: list[Request]) -> None:
         pending = self.sampler.defer_batch(logits, [r.params for r in rows])
         ahead_rows, self._pending_rows = self._pending_rows, None
+        inflight = None
         if ahead_rows is not None:
             self._prepare_ahead(ahead_rows)
+            inflight = self._launch_ahead(pending, ahead_rows)
         ids = pending.finish()
         now = time.perf_counter()
         done = []
@@ -388,6 +429,7 @@ class Engine:
             self.finished.append(req)
             self.pages.release(req.pages)
             req.pages = []
+        self._inflight = inflight
 
     # ------------------------------------------------------------------ graphs
     def _bucket_sizes(self) -> list[int]:
@@ -480,7 +522,21 @@ class Engine:
     # ------------------------------------------------------------------ loop
     def step(self) -> None:
         """Prefill, then decode every running request (``scheduler.rs:204-271`` step_serial);
-        a step whose prefill ran a chunk that is not its request's last ends there."""
+        a step whose prefill ran a chunk that is not its request's last ends there. A decode
+        step launched ahead by the previous step (``_launch_ahead``) is this step's decode: its
+        tokens are sampled and committed, and it may launch its own successor. If one of its
+        rows ended on an end-of-sequence token meanwhile, the launched step is dropped and the
+        live rows decode again (its K/V writes are rewritten with the same values)."""
+        if self._inflight is not None:
+            fl, self._inflight = self._inflight, None
+            if all(not r.finished() for r in fl.rows):
+                self.stats["decode_steps"] += 1
+                self.stats["graph_steps"] += 1
+                self.stats["ahead_steps"] += 1
+                self.stats["overlap_steps"] += 1
+                self._pending_rows = fl.rows
+                self._sample_and_commit(fl.graph.logits[:len(fl.rows)], fl.rows)
+                return
         picked = self._select_prefill()
         if picked:
             self._run_prefill(picked)

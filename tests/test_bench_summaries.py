@@ -52,7 +52,12 @@ def test_gap_summary_splits_stretches_at_host_pauses(tmp_path):
         t += 10 ** 9  # a one-second host pause
     _write(path, ["Kernel_Name", "Start_Timestamp", "End_Timestamp"], rows)
     lines = bench.summarize_gaps(str(path)).splitlines()
-    assert len(lines) == 3
     first, second = lines[1].split(), lines[2].split()
     assert first[1] == second[1] == "1200" and first[2] == "120"
     assert float(first[6]) == 1.0 and float(second[6]) == 0.5
+    # Idle time by the kernel it follows: in the first run 120 gaps of 1 us follow the
+    # decode kernel and 1079 follow the others.
+    i = lines.index("# stretch 0: idle time by the kernel it follows (top 8)")
+    table = {ln.split()[0]: ln.split() for ln in lines[i + 2:i + 4]}
+    assert table["other"][3] == "1079" and table["decode_mma_kernel<0>"][3] == "120"
+    assert float(table["decode_mma_kernel<0>"][1]) == 0.12

@@ -262,8 +262,8 @@ def test_staged_decode_step_is_discarded_when_a_request_arrives(gpu):
         reqs = [eng.add_request(p, SamplingParams(max_tokens=9)) for p in first]
         for _ in range(4):  # one prefill step, then decode steps that stage their successors
             eng.step()
-        if staged:
-            assert eng._ahead is not None  # a step is staged when the request arrives
+        if staged:  # a step is staged (or already launched) when the request arrives
+            assert eng._ahead is not None or eng._inflight is not None
         reqs.append(eng.add_request(late, SamplingParams(max_tokens=9)))
         eng.run_until_complete()
         out = [list(r.output) for r in reqs]
@@ -276,6 +276,45 @@ def test_staged_decode_step_is_discarded_when_a_request_arrives(gpu):
     staged, stats = run(True)
     assert staged == plain and all(len(o) == 9 for o in staged)
     assert stats["ahead_steps"] > 0
+
+
+def test_overlapped_decode_matches_serial(gpu):
+    """The overlap of consecutive decode steps (``scheduler.rs:935-1000``): the next graph step
+    is launched with its input tokens fed on the device before the host reads them. Tokens must
+    equal the serial engine's under temperature/top-k/top-p sampling (same sampling calls, same
+    rows, same seed offsets), with requests ending by length at different steps and one ending
+    on its end-of-sequence token (the launched step is dropped and the live rows decode
+    again)."""
+    model, _ = build(TINY, 17, gpu)
+    rng = np.random.default_rng(19)
+    prompts = [rng.integers(0, TINY.vocab_size, n) for n in (11, 27, 18, 33)]
+    budgets = (12, 9, 14, 12)
+
+    def run(overlap, eos=None):
+        eng = Engine(model, EngineConfig(max_running_req=8, max_seq_len=128, seed=7,
+                                         graph_batch_sizes=(4, 8), overlap_decode=overlap))
+        reqs = [eng.add_request(p, SamplingParams(temperature=0.7, top_k=20, top_p=0.9,
+                                                  max_tokens=m),
+                                eos_token_id=eos if i == 2 else None)
+                for i, (p, m) in enumerate(zip(prompts, budgets))]
+        eng.run_until_complete()
+        out = [list(r.output) for r in reqs]
+        stats = dict(eng.stats)
+        del eng
+        torch.cuda.synchronize()
+        return out, stats
+
+    serial, st_serial = run(False)
+    overlapped, st = run(True)
+    assert st_serial["overlap_steps"] == 0 and st["overlap_steps"] > 0
+    assert st["graph_steps"] == st["decode_steps"] == st_serial["decode_steps"]
+    assert overlapped == serial
+    assert [len(o) for o in overlapped] == list(budgets)
+    stop = next(i for i in range(3, 10) if serial[2][i] not in serial[2][:i])
+    cut_serial, _ = run(False, eos=serial[2][stop])
+    cut, st_cut = run(True, eos=serial[2][stop])
+    assert cut == cut_serial and cut[2] == serial[2][:stop + 1]
+    assert st_cut["overlap_steps"] > 0
 
 
 def test_non_final_prefill_chunk_ends_the_step(gpu):
