@@ -90,6 +90,28 @@ def test_decode_schedule_cuts_on_tiles(native):
     assert n == 256 and all(c == 1 for c in merge[1::2])
 
 
+def test_decode_schedule_randomized_batches(native):
+    """The tile-counted share search and the whole-request placement over a wide spread of
+    batches: a few very long requests, many one-token requests, mixtures, up to 2,048 rows."""
+    rng = np.random.default_rng(31)
+    for case in range(120):
+        b = int(rng.choice([1, 2, 5, 17, 64, 200, 256, 257, 700, 2048]))
+        kind = case % 4
+        if kind == 0:
+            lengths = rng.integers(1, 17, size=b)
+        elif kind == 1:
+            lengths = rng.integers(1, 1 << 20, size=b) if b <= 17 else rng.integers(1, 9000, size=b)
+        elif kind == 2:
+            lengths = 1280 + rng.integers(-40, 41, size=b)
+        else:
+            lengths = np.where(rng.random(b) < 0.1, rng.integers(4000, 70000, size=b),
+                               rng.integers(1, 300, size=b))
+        lengths = lengths.astype(int).tolist()
+        n, work, merge, chunk, cap = _schedule(native, lengths)
+        assert 0 < n <= cap, (case, b, kind)
+        oplan.check_work_list(work, merge, lengths)
+
+
 def test_decode_schedule_rejects_bad_input(native):
     lib = native.lib()
     lens = (ctypes.c_int32 * 2)(5, 0)

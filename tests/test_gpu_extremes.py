@@ -3,7 +3,8 @@
 * a 131,072-token decode context next to 1-17 token requests (page sizes 1 and 16; the long
   request is cut into many work items because one item's page entries must fit in LDS);
 * the full 256-request decode batch at the Qwen3-8B serving shape (page 16, GQA group 4,
-  KV lengths 1024-1536, the largest captured decode-graph bucket);
+  KV lengths 1024-1536, the largest captured decode-graph bucket), and the same batch at nearly
+  equal lengths, which the planner places as whole requests;
 * paged prefill over a 65,536-token cached prefix next to a 1-token prefix and a 1-token
   extend (query rows sampled: first, last and random);
 * two decode plans and a prefill plan on three concurrent streams, equal to serial runs.
@@ -88,6 +89,17 @@ def test_decode_full_batch_at_serving_shape(gpu):
     lengths = rng.integers(1024, 1537, size=256)
     got, want, _ = run_decode(gpu, 32, 8, 16, lengths, 256)
     assert_close(got, want, "batch 256 page 16 group 4")
+
+
+def test_decode_whole_requests_at_near_equal_lengths(gpu):
+    """256 requests of 1,248-1,312 tokens (the config-5 decode steps): the planner places whole
+    requests (no split, so no partials and no merge launch) instead of cutting requests to even
+    out a tile or two; the result must still match the oracle."""
+    rng = np.random.default_rng(1280)
+    lengths = 1280 + rng.integers(-32, 33, size=256)
+    got, want, md = run_decode(gpu, 32, 8, 16, lengths, 1280)
+    assert len(md["work"]) // 4 == 256 and all(c == 1 for c in md["merge"][1::2])
+    assert_close(got, want, "batch 256 whole requests")
 
 
 def test_paged_prefill_64k_prefix_sampled_rows(gpu):
