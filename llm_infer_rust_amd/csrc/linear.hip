@@ -281,35 +281,48 @@ __global__ __launch_bounds__(256) void linear_reduce(const float* __restrict__ p
 // chunk c + 256 j per lane and the same two-level sum of squares as the stand-alone
 // residual RMSNorm for these widths, so the results equal the two separate passes bit for
 // bit.
-template <int DT, int NCH, bool PARTIAL>
+// SPLITS > 0: that many K splits, all partial loads (and the residual and weight loads)
+// issued before the first sum, so a row costs one memory round trip; 0: any count, read
+// split after split.
+template <int DT, int NCH, bool PARTIAL, int SPLITS>
 __global__ __launch_bounds__(256) void reduce_add_rms(const float* __restrict__ partial,
                                                       int splits, uint16_t* out, int64_t ldo,
                                                       uint16_t* residual, int64_t ldr,
                                                       const uint16_t* __restrict__ weight,
                                                       int M, int N, float eps) {
+  constexpr int kHeld = SPLITS > 0 ? SPLITS : 1;
   __shared__ float wave_ss[4];
   const int64_t row = blockIdx.x;
   const int chunks = N >> 3;
   const int64_t plane = static_cast<int64_t>(M) * N;
   float vals[NCH][8];
-  uint4 wraw[NCH];
+  uint4 wraw[NCH], rraw[NCH], oraw[NCH];
+  float4 part[NCH][kHeld][2];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int chunk = threadIdx.x + c * 256;
-    if (chunk < chunks) wraw[c] = ld128(weight + chunk * 8);
+    if (chunk >= chunks) continue;
+    wraw[c] = ld128(weight + chunk * 8);
+    if constexpr (PARTIAL) {
+      const float* p = partial + row * N + chunk * 8;
+#pragma unroll
+      for (int k = 0; k < kHeld; ++k) {
+        part[c][k][0] = *reinterpret_cast<const float4*>(p + k * plane);
+        part[c][k][1] = *reinterpret_cast<const float4*>(p + k * plane + 4);
+      }
+    } else {
+      oraw[c] = ld128(out + row * ldo + chunk * 8);
+    }
+    rraw[c] = ld128(residual + row * ldr + chunk * 8);
   }
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int chunk = threadIdx.x + c * 256;
     if (chunk >= chunks) continue;
     if constexpr (PARTIAL) {
-      const float* p = partial + row * N + chunk * 8;
-      float4 lo = *reinterpret_cast<const float4*>(p);
-      float4 hi = *reinterpret_cast<const float4*>(p + 4);
-      for (int k = 1; k < splits; ++k) {
-        const float4 a = *reinterpret_cast<const float4*>(p + k * plane);
-        const float4 b = *reinterpret_cast<const float4*>(p + k * plane + 4);
+      float4 lo = part[c][0][0], hi = part[c][0][1];
+      auto add = [&](const float4& a, const float4& b) {
         lo.x += a.x;
         lo.y += a.y;
         lo.z += a.z;
@@ -318,14 +331,23 @@ __global__ __launch_bounds__(256) void reduce_add_rms(const float* __restrict__ 
         hi.y += b.y;
         hi.z += b.z;
         hi.w += b.w;
+      };
+      if constexpr (SPLITS > 0) {
+#pragma unroll
+        for (int k = 1; k < SPLITS; ++k) add(part[c][k][0], part[c][k][1]);
+      } else {
+        const float* p = partial + row * N + chunk * 8;
+        for (int k = 1; k < splits; ++k)
+          add(*reinterpret_cast<const float4*>(p + k * plane),
+              *reinterpret_cast<const float4*>(p + k * plane + 4));
       }
       const float y[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       unpack8<DT>(pack8<DT>(y), vals[c]);  // the projection's output, rounded once
     } else {
-      unpack8<DT>(ld128(out + row * ldo + chunk * 8), vals[c]);
+      unpack8<DT>(oraw[c], vals[c]);
     }
     float r[8];
-    unpack8<DT>(ld128(residual + row * ldr + chunk * 8), r);
+    unpack8<DT>(rraw[c], r);
 #pragma unroll
     for (int i = 0; i < 8; ++i) vals[c][i] += r[i];
     st128(residual + row * ldr + chunk * 8, pack8<DT>(vals[c]));
@@ -351,21 +373,39 @@ __global__ __launch_bounds__(256) void reduce_add_rms(const float* __restrict__ 
   }
 }
 
+template <int DT, int NCH, bool PARTIAL>
+void launch_reduce_add_rms_splits(const float* partial, int splits, uint16_t* out, int64_t ldo,
+                                  uint16_t* residual, int64_t ldr, const uint16_t* weight,
+                                  int M, int N, float eps, hipStream_t s) {
+  const dim3 grid(static_cast<uint32_t>(M)), block(256);
+#define MI355X_REDUCE_ADD_RMS(S)                                                            \
+  reduce_add_rms<DT, NCH, PARTIAL, S><<<grid, block, 0, s>>>(partial, splits, out, ldo,    \
+                                                             residual, ldr, weight, M, N, eps)
+  if (!PARTIAL || splits == 1)
+    MI355X_REDUCE_ADD_RMS(1);
+  else if (splits == 2)
+    MI355X_REDUCE_ADD_RMS(2);
+  else if (splits == 4)
+    MI355X_REDUCE_ADD_RMS(4);
+  else
+    MI355X_REDUCE_ADD_RMS(0);
+#undef MI355X_REDUCE_ADD_RMS
+}
+
 template <int DT, bool PARTIAL>
 void launch_reduce_add_rms(const float* partial, int splits, uint16_t* out, int64_t ldo,
                            uint16_t* residual, int64_t ldr, const uint16_t* weight, int M, int N,
                            float eps, hipStream_t s) {
   const int chunks = N / 8;
-  const dim3 grid(static_cast<uint32_t>(M)), block(256);
   if (chunks <= 256)
-    reduce_add_rms<DT, 1, PARTIAL><<<grid, block, 0, s>>>(partial, splits, out, ldo, residual,
-                                                           ldr, weight, M, N, eps);
+    launch_reduce_add_rms_splits<DT, 1, PARTIAL>(partial, splits, out, ldo, residual, ldr,
+                                                 weight, M, N, eps, s);
   else if (chunks <= 512)
-    reduce_add_rms<DT, 2, PARTIAL><<<grid, block, 0, s>>>(partial, splits, out, ldo, residual,
-                                                           ldr, weight, M, N, eps);
+    launch_reduce_add_rms_splits<DT, 2, PARTIAL>(partial, splits, out, ldo, residual, ldr,
+                                                 weight, M, N, eps, s);
   else
-    reduce_add_rms<DT, 4, PARTIAL><<<grid, block, 0, s>>>(partial, splits, out, ldo, residual,
-                                                           ldr, weight, M, N, eps);
+    launch_reduce_add_rms_splits<DT, 4, PARTIAL>(partial, splits, out, ldo, residual, ldr,
+                                                 weight, M, N, eps, s);
 }
 
 struct TileConfig {
