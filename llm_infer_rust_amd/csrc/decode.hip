@@ -17,10 +17,12 @@
 //   last_page_len[r] = (len[r] - 1) % P + 1
 //
 // Split-KV schedule (our own design for 256 CUs): the grid's workgroups each take
-// an equal share of all tokens of the batch ("stream-K" over the flattened token
-// list); the requests a share touches become its work items. A request held by one
-// item writes its output directly; a request cut into several items writes
-// normalised fp32 partials + log2-sum-exp that a small merge kernel combines.
+// an equal share of the batch's work, counted in the kernel's 16-token tiles plus a
+// fixed cost per work item ("stream-K" over the flattened tile list), or whole
+// requests when that is cheaper than the split and its merge launch; the requests a
+// share touches become its work items. A request held by one item writes its output
+// directly; a request cut into several items writes normalised fp32 partials +
+// log2-sum-exp that a small merge kernel combines.
 // (Merging inside the last-arriving workgroup needs an agent-scope release per
 // workgroup, i.e. an L2 write-back on every XCD, and measured ~5x slower than the
 // extra launch.)
