@@ -44,6 +44,7 @@ constexpr int kWarps = kThreads / kWave;
 constexpr int kBins0 = 4096;  // bits 30..19 of p (bit 31, the sign, is always 0)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kFixedScale = 1099511627776.0f;  // 2^40
+constexpr uint32_t kCandidates = 2048;  // candidate path: (index, s, p) lists in LDS
 
 // Logits element access for dtype codes 0 (bf16), 1 (fp16), 2 (fp32).
 template <int DT>
@@ -108,6 +109,15 @@ struct Shared {
   unsigned long long p_rem;
   int p_found, k_found, k_active;
 };
+
+// Unsigned key that orders like the float value (non-NaN): larger s, larger key.
+__device__ __forceinline__ uint32_t order_key(float s) {
+  const uint32_t u = __float_as_uint(s);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t key) {
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
 
 __device__ __forceinline__ bool better(float v, int64_t i, float bv, int64_t bi) {
   // Larger value wins, NaN beats everything, lower index breaks ties.
@@ -269,11 +279,19 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a, bool vec
     return;
   }
 
+  // Top-k rows first try a shorter route (the candidate path below); pass 1 then also
+  // counts the scaled logits in 4,096 bins of their top order-key bits.
+  const bool fast_k = top_k < vocab;
+  if (fast_k) {
+    for (int b = threadIdx.x; b < kBins0; b += kThreads) sh.cnt[b] = 0;
+    __syncthreads();
+  }
   // Pass 1: max and sum of exp(s - max).
   float m = -INFINITY, z = 0.f;
   bool nan_seen = false;
   for_each<DT>(a, row, vec, [&](int64_t, float x) {
     const float s = scaled(x);
+    if (fast_k && s == s && s != -INFINITY) atomicAdd(&sh.cnt[order_key(s) >> 20], 1u);
     if (s != s) {
       nan_seen = true;
       return;
@@ -314,17 +332,150 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a, bool vec
   }
   const float inv_z = 1.f / z;
   auto prob = [&](float s) { return exp2f((s - m) * kLog2e) * inv_z; };
+  auto fixed = [](float p) { return static_cast<unsigned long long>(p * kFixedScale + 0.5f); };
+  const bool use_p = top_p < 1.f;
+  const unsigned long long p_target = [&] {
+    const unsigned long long t = static_cast<unsigned long long>(top_p * kFixedScale);
+    return t ? t : 1ull;  // at least one unit, so the top bin is always selectable
+  }();
+
+  // Candidate path (top-k rows): the order-key histogram of pass 1 gives the bin b1 that
+  // holds the k-th largest scaled logit. Every token with s >= s_lo (the bin's lower edge
+  // less a margin far above the rounding of p) is a candidate, and every other token's p is
+  // below every candidate's that lies in or above b1, so the k-th largest p of the row, the
+  // top-p cutoff at or above it (its mass in the same 2^-40 fixed point) and the survivors
+  // are all found among the candidates, which are gathered once into LDS. Exactly the
+  // cutoffs and draw of the radix path below; that path runs when the candidates do not
+  // fit (heavy ties), a row has fewer than k finite logits, or the k-th p has no fixed-point
+  // mass. Two row passes instead of four, one of them without exponentials.
+  if (fast_k) {
+    // Bin b1 from the top, through the same thread-owns-4-bins suffix scan as below.
+    const int b0 = threadIdx.x * 4;
+    uint32_t c4[4];
+    for (int j = 0; j < 4; ++j) c4[j] = sh.cnt[b0 + j];
+    uint32_t csum = c4[0] + c4[1] + c4[2] + c4[3];
+    unsigned long long zero = 0;
+    uint32_t total_c;
+    unsigned long long total_m;
+    block_scan(sh, csum, zero, total_c, total_m);
+    uint32_t c_above = total_c - csum;
+    if (threadIdx.x == 0) sh.k_found = 0;
+    __syncthreads();
+    for (int j = 3; j >= 0; --j) {
+      if (c4[j] && c_above < static_cast<uint32_t>(top_k) &&
+          c_above + c4[j] >= static_cast<uint32_t>(top_k)) {
+        sh.k_prefix = static_cast<uint32_t>(b0 + j);
+        sh.k_rem = c_above + c4[j];  // tokens in bins b1 and above
+        sh.k_found = 1;
+      }
+      c_above += c4[j];
+    }
+    __syncthreads();
+    bool ok = sh.k_found && sh.k_rem <= kCandidates;
+    if (ok) {
+      const float s_lower = key_value(sh.k_prefix << 20);
+      const float s_lo = s_lower - (fabsf(s_lower - m) + 1.f) * 0x1p-12f;
+      uint32_t* cand_i = reinterpret_cast<uint32_t*>(sh.mass);
+      float* cand_s = reinterpret_cast<float*>(cand_i + kCandidates);
+      float* cand_p = cand_s + kCandidates;
+      if (threadIdx.x == 0) sh.p_lowest = 0;  // candidate count
+      __syncthreads();
+      for_each<DT>(a, row, vec, [&](int64_t i, float x) {
+        const float s = scaled(x);
+        if (!(s >= s_lo) || s == -INFINITY) return;
+        const uint32_t slot = atomicAdd(&sh.p_lowest, 1u);
+        if (slot < kCandidates) {
+          cand_i[slot] = static_cast<uint32_t>(i);
+          cand_s[slot] = s;
+        }
+      });
+      __syncthreads();
+      const uint32_t n = sh.p_lowest;
+      ok = n <= kCandidates;
+      if (ok) {
+        for (uint32_t t = threadIdx.x; t < n; t += kThreads) cand_p[t] = prob(cand_s[t]);
+        __syncthreads();
+        // The k-th largest p: the candidate value v with #(p > v) < k <= #(p >= v).
+        if (threadIdx.x == 0) sh.k_found = 0;
+        __syncthreads();
+        for (uint32_t t = threadIdx.x; t < n; t += kThreads) {
+          const float v = cand_p[t];
+          uint32_t gt = 0, ge = 0;
+          for (uint32_t u = 0; u < n; ++u) {
+            gt += cand_p[u] > v;
+            ge += cand_p[u] >= v;
+          }
+          if (gt < static_cast<uint32_t>(top_k) && ge >= static_cast<uint32_t>(top_k)) {
+            sh.red_f[0] = v;  // every thread that gets here writes the same value
+            sh.k_found = 1;
+          }
+        }
+        __syncthreads();
+        const float p_k = sh.red_f[0];
+        ok = sh.k_found && !(use_p && fixed(p_k) == 0);
+        float cut = p_k;
+        if (ok && use_p) {
+          // Mass at or above p_k; when it reaches top_p, the top-p cutoff is the largest
+          // candidate value whose mass at or above reaches it.
+          unsigned long long mk = 0;
+          for (uint32_t t = threadIdx.x; t < n; t += kThreads)
+            if (cand_p[t] >= p_k) mk += fixed(cand_p[t]);
+          uint32_t zc = 0;
+          uint32_t tc;
+          unsigned long long tm;
+          block_scan(sh, zc, mk, tc, tm);
+          if (tm >= p_target) {
+            float best_v = p_k;
+            for (uint32_t t = threadIdx.x; t < n; t += kThreads) {
+              const float v = cand_p[t];
+              if (v < p_k) continue;
+              unsigned long long mv = 0;
+              for (uint32_t u = 0; u < n; ++u)
+                if (cand_p[u] >= v) mv += fixed(cand_p[u]);
+              if (mv >= p_target) best_v = fmaxf(best_v, v);
+            }
+            float bv = best_v;
+            int64_t bi = 0;
+            block_argmax(sh, bv, bi);
+            cut = bv;
+          }
+        }
+        if (ok) {
+          // The race over the surviving candidates (order-independent: larger key, then
+          // lower index).
+          float best = -INFINITY;
+          int64_t best_i = vocab;
+          for (uint32_t t = threadIdx.x; t < n; t += kThreads) {
+            const float pt = cand_p[t];
+            if (!(pt > 0.f && pt >= cut)) continue;
+            const int64_t i = cand_i[t];
+            const uint4 rnd =
+                philox4x32_10(make_uint4(static_cast<uint32_t>(i >> 2), static_cast<uint32_t>(row),
+                                         a.offset_lo, a.offset_hi),
+                              k0, k1);
+            const uint32_t words[4] = {rnd.x, rnd.y, rnd.z, rnd.w};
+            const float key = cand_s[t] + gumbel(words[i & 3]);
+            if (key > best || (key == best && i < best_i)) {
+              best = key;
+              best_i = i;
+            }
+          }
+          block_argmax(sh, best, best_i);
+          if (threadIdx.x == 0) a.out[row] = best_i < vocab ? best_i : -1;
+          return;
+        }
+      }
+    }
+    __syncthreads();  // the candidate lists alias the mass histogram of the radix path
+  }
 
   // Passes 2-4: radix selection of the two cutoffs over the bits of p.
-  const bool use_p = top_p < 1.f;
   if (threadIdx.x == 0) {
     sh.k_prefix = 0;
     sh.k_rem = static_cast<uint32_t>(top_k);
     sh.k_active = top_k < vocab;
     sh.p_prefix = 0;
-    // At least one unit, so the top bin is always selectable.
-    const unsigned long long target = static_cast<unsigned long long>(top_p * kFixedScale);
-    sh.p_rem = target ? target : 1ull;
+    sh.p_rem = p_target;
   }
   constexpr int kShift[3] = {19, 9, 0};
   constexpr int kBits[3] = {12, 10, 9};
