@@ -872,7 +872,8 @@ def serving_ops_section(dev, reps: int, cpu: bool = True) -> dict:
     res = {"us": round(ms * 1e3, 2), "rows/s": round(rows / (ms * 1e-3), 1), "bytes": nbytes,
            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
            "note": "eager calls through Sampler (host parameter handling included); bytes are "
-                   "one pass over the logits, the kernel makes up to five (the row stays in L2)"}
+                   "one pass over the logits; the kernel makes two for top-k rows, up to five "
+                   "otherwise (the row stays in L2)"}
     if cpu:
         from oracle import sampling as osamp  # the CPU baseline only
         sample = logits[:8].float().cpu().numpy()
