@@ -61,7 +61,13 @@ struct Logit<2> {
   using Word = float;
   static constexpr int kVec = 4;
   __device__ __forceinline__ static float to_float(Word w) { return w; }
-  __device__ __forceinline__ static float round(float f) { return f; }
+  // The scaled logit must be the rounded product: without the barrier the compiler may fuse
+  // x * (1 / T) into a later s - max as one fma, which differs from the rounded s by up to half
+  // an ulp, and can differ between the passes (the top token's p then missing its own cutoff).
+  __device__ __forceinline__ static float round(float f) {
+    asm volatile("" : "+v"(f));
+    return f;
+  }
 };
 
 // Philox4x32-10 (Random123): 10 rounds, key schedule bumped between rounds.

@@ -6,6 +6,8 @@ and 736-757 (the joint 3/7 case). Beyond those, every row of a wide random batch
 oracle's draw for the same (seed, offset) exactly, unless the oracle reports a float-level near
 tie for that row.
 """
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -136,3 +138,49 @@ def test_unaligned_rows_use_the_scalar_path(gpu):
                                       11, 0)
     for r in range(8):
         assert ids[r] == want[r] or margins[r] < 1e-4
+
+
+def _edge_rows(case, vocab, g):
+    """Rows that steer top-k sampling onto each branch of the candidate path and its fallbacks."""
+    x = torch.randn(8, vocab, generator=g)
+    if case == "ties":  # 5 distinct logits: the k-th value's bin holds thousands of tokens
+        return torch.round(x).clamp(-2, 2)
+    if case == "ties_fit":  # ~20 distinct logits: ties at the k-th value that still fit the list
+        return torch.round(x * 2) / 2
+    if case == "few_finite":  # 30 or 60 finite logits against k = 50
+        keep = torch.zeros(8, vocab, dtype=torch.bool)
+        for r in range(8):
+            keep[r, torch.randperm(vocab, generator=g)[: 30 if r % 2 == 0 else 60]] = True
+        return torch.where(keep, x, torch.full_like(x, float("-inf")))
+    if case == "sharp":  # the k-th largest p underflows to zero (mass and value)
+        return x * 200
+    if case == "negative":
+        return x - 50
+    if case == "coarse":  # large offset: bf16 spacing 4-8 makes many exact ties near the top
+        return x * 30 + 1000
+    return x * 3
+
+
+@pytest.mark.parametrize("dtype,name", [(torch.bfloat16, "bf16"), (torch.float32, None)])
+@pytest.mark.parametrize("case,k,p", [
+    ("ties", 50, 0.9), ("ties", 1, 1.0), ("ties_fit", 50, 0.9), ("ties_fit", 3000, 0.95),
+    ("plain", 2000, 0.95), ("plain", 2048, 1.0), ("plain", 2049, 0.99), ("plain", 4000, 0.9),
+    ("plain", 50, 1e-9), ("few_finite", 50, 0.9), ("few_finite", 50, 1.0),
+    ("sharp", 50, 0.9), ("sharp", 50, 1.0), ("negative", 50, 0.9), ("coarse", 20, 0.8)])
+def test_top_k_candidate_path_edges_match_oracle(gpu, dtype, name, case, k, p):
+    """Top-k rows first try a candidate list gathered from an order-key histogram and fall back
+    to the radix selection when the list overflows (heavy ties), a row has fewer than k finite
+    logits or the k-th p has no fixed-point mass; every branch must give the oracle's draw."""
+    vocab = 151936
+    g = torch.Generator().manual_seed(zlib.crc32(f"{case}/{k}".encode()))
+    logits = _edge_rows(case, vocab, g).to(dtype)
+    rows = logits.shape[0]
+    s = Sampler(77)
+    s.offset = 3
+    ids = s.sample_batch_device(logits.to(gpu), [sp(0.7, k, p)] * rows).cpu().numpy()
+    round_to = (lambda v: obf.round_to(v, name)) if name else None
+    want, margins = osamp.sample_rows(logits.float().numpy(), [0.7] * rows, [k] * rows,
+                                      [p] * rows, 77, 3, round_to)
+    for r in range(rows):
+        if ids[r] != want[r]:
+            assert margins[r] < 1e-4, (case, k, p, r, ids[r], want[r], margins[r])
