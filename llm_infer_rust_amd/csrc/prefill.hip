@@ -98,16 +98,6 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 }
 
 
-// Eight 16-bit values times c, rounded back to the element type (round to nearest even).
-template <int DT>
-__device__ __forceinline__ uint4 scale_row8(const uint4& x, float c) {
-  auto sc = [&](uint32_t w) {
-    return Elem<DT>::pack2(Elem<DT>::to_float(static_cast<uint16_t>(w & 0xffff)) * c,
-                           Elem<DT>::to_float(static_cast<uint16_t>(w >> 16)) * c);
-  };
-  return make_uint4(sc(x.x), sc(x.y), sc(x.z), sc(x.w));
-}
-
 // ---------------------------------------------------------------------------
 // Tile staging. K and V tiles are copied global -> LDS by the
 // load engine (global_load_lds_dwordx4: each lane's 16 bytes land at
@@ -200,13 +190,12 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void prefill_kernel(Prefi
 #pragma unroll
     for (int s = 0; s < 8; ++s) qreg[s] = ld128(qp + 16 * s + 8 * half);
     wait_vmem_loads();
-    // Fold the softmax scale (and log2 e) into the query once per item, so the tile
-    // loop's scores come out of the matrix cores already in the exp2 domain.
-#pragma unroll
-    for (int s = 0; s < 8; ++s) qreg[s] = scale_row8<DT>(qreg[s], a.scale_log2);
-    // Keep the scaled rows in registers behind an empty asm the compiler cannot look
-    // through, so the scaling can never be rematerialised inside the tile loop (at 250+
-    // VGPRs that would be the cheap way out for the register allocator).
+    // The query rows enter the matrix cores as they are: the softmax scale (and log2 e) is
+    // applied to the fp32 scores. Folding it into the rows would round q * scale to the
+    // input type, a score error that grows with the size of the products q_d k_d.
+    // Keep the rows in registers behind an empty asm the compiler cannot look through, so
+    // they are never reloaded inside the tile loop (at 250+ VGPRs that would be the cheap
+    // way out for the register allocator).
 #pragma unroll
     for (int s = 0; s < 8; ++s)
       asm volatile("" : "+v"(qreg[s].x), "+v"(qreg[s].y), "+v"(qreg[s].z), "+v"(qreg[s].w));
@@ -338,8 +327,10 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void prefill_kernel(Prefi
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
-  // m: this lane's reference max (log2 domain); every S^T accumulator starts at -m,
-  // so the scores leave the matrix cores as s - m and p = 2^(s - m) needs no VALU fma.
+  // m: this lane's reference max of the raw scores q.k; every S^T accumulator starts at -m,
+  // so the scores leave the matrix cores as s - m and p = 2^(c (s - m)), c = scale * log2 e.
+  const float c = a.scale_log2;
+  const float lazy_limit = 8.f / c;  // 2^8 in p
   float m = 0.f, l = 0.f;
   floatx16 negm;
 #pragma unroll
@@ -398,13 +389,15 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void prefill_kernel(Prefi
       mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max of s - m
     }
     // Lazy rescale: m moves on the first tile (to the row max) and afterwards only when
-    // some row's max exceeds it by more than 8, so p = 2^(s - m) <= 2^8 and O / l are
-    // rescaled rarely. The first tile of a whole item holds key 0, which each query sees,
+    // some row's max exceeds it by more than 8 / c, so p = 2^(c (s - m)) <= 2^8 and O / l
+    // are rescaled rarely. The first tile of a whole item holds key 0, which each query sees,
     // so mx is finite there; the first tile of a later chunk can lie wholly past a query's
     // horizon (mx = -inf), and that row then keeps m = 0 until a key reaches it.
-    if (first || __any(mx > 8.f)) {
+    if (first || __any(mx > lazy_limit)) {
       const float shift = first ? (mx == -INFINITY ? 0.f : mx) : fmaxf(mx, 0.f);
-      const float alpha = __builtin_amdgcn_exp2f(-shift);
+      // Nothing is accumulated before the first tile; its shift can be any size (every
+      // score far below zero makes 2^-shift overflow, and 0 * inf would be NaN).
+      const float alpha = first ? 1.f : __builtin_amdgcn_exp2f(-shift * c);
       m += shift;
       l *= alpha;
 #pragma unroll
@@ -427,7 +420,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void prefill_kernel(Prefi
         float p[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          p[i] = __builtin_amdgcn_exp2f(s[T][8 * hh + i]);
+          p[i] = __builtin_amdgcn_exp2f(s[T][8 * hh + i] * c);
           ls[i & 3] += p[i];
         }
         pb[2 * T + hh] = make_uint4(pack2<DT>(p[0], p[1]), pack2<DT>(p[2], p[3]),
@@ -472,7 +465,7 @@ __global__ __launch_bounds__(64 * NW, NW == 8 ? 1 : 2) void prefill_kernel(Prefi
                         o[db][4 * g4 + 3] * inv);
     if (half == 0)
       a.part_lse[rec * kQPerWave + col] =
-          row_sum > 0.f ? m + __builtin_amdgcn_logf(row_sum) : -INFINITY;
+          row_sum > 0.f ? m * c + __builtin_amdgcn_logf(row_sum) : -INFINITY;
     return;
   }
   // The wave's 32 x 128 output tile goes out as whole 256-byte rows: written to an LDS

@@ -1,0 +1,181 @@
+"""Attention on extreme score distributions: prefill and decode against the float64 oracle.
+
+The random N(0,1) cases elsewhere keep every score within a few units of the row max. Here the
+scores are built along one direction u of the 128-dim head space (q = c u + noise, k_j = a_j u +
+noise), so that the online softmax meets what real prompts can produce:
+  climb      the max grows along the keys by 6-26 score units per 64-key tile (the prefill
+             kernel's lazy rescale, which renormalises only when the max grows by more than
+             2^8, fires on many tiles; decode's split items see different maxima per item);
+  first      key 0 scores ~150 above every other key (everything else underflows);
+  late       one key in the middle scores ~150 above the rest (the max jumps mid-row, the
+             earlier accumulators rescale by ~2^-216);
+  negative   every score near -500 (softmax is shift-invariant; the running max starts at
+             -inf);
+  sharp      q and k ~ N(0, 3^2): score spread ~9 units, random peaks.
+Tolerance as in the other attention tests: max-abs <= 2e-2 and cosine > 0.9999 against the
+float64 oracle on the same rounded inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from llm_infer_rust_amd.backend import Attention, AttentionMetadata, AttentionSpec, BatchPhase
+from llm_infer_rust_amd.kv_cache import BaseAttention
+from oracle import attention as oatt
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MIN_COS = 0.9999
+D = 128
+PATTERNS = ["climb", "first", "late", "negative", "sharp"]
+
+
+def f32(t):
+    return t.float().cpu().numpy()
+
+
+def assert_close(got, want, what=""):
+    got = np.asarray(got, np.float64).ravel()
+    want = np.asarray(want, np.float64).ravel()
+    err = float(np.abs(got - want).max())
+    cs = float(got @ want / (np.linalg.norm(got) * np.linalg.norm(want) + 1e-30))
+    assert err <= MAX_ABS and cs > MIN_COS, f"{what} max_abs={err} cos={cs}"
+
+
+def _direction(g):
+    u = torch.randn(D, generator=g)
+    return u / u.norm()
+
+
+def keys_for(pattern, length, heads, u, g, slope):
+    """Keys of one sequence, [length, heads, D], with the along-u component a_j of `pattern`
+    (scores are ~ a_j * c / sqrt(D) for queries with along-u component c)."""
+    noise = torch.randn(length, heads, D, generator=g)
+    if pattern == "sharp":
+        return noise * 3
+    pos = torch.arange(length, dtype=torch.float32)
+    if pattern == "climb":
+        a = pos * slope
+    elif pattern == "first":
+        a = torch.where(pos == 0, torch.tensor(150.0), torch.tensor(0.0))
+    elif pattern == "late":
+        a = torch.where(pos == length // 2, torch.tensor(150.0), torch.tensor(0.0))
+    else:  # negative
+        a = torch.full((length,), -500.0)
+    return noise + a.view(-1, 1, 1) * u
+
+
+def queries_for(pattern, rows, heads, u, g):
+    noise = torch.randn(rows, heads, D, generator=g)
+    if pattern == "sharp":
+        return noise * 3
+    return noise * 0.1 + u * D ** 0.5  # c = sqrt(D): score = a_j along u
+
+
+@pytest.mark.parametrize("pattern", PATTERNS)
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8)])
+def test_ragged_prefill_extreme_scores(gpu, pattern, hq, hkv):
+    g = torch.Generator().manual_seed(len(pattern) * 31 + hq)
+    u = _direction(g)
+    lens = [37, 663, 700, 1]
+    bounds = [0] + np.cumsum(lens).tolist()
+    n = bounds[-1]
+    k = torch.cat([keys_for(pattern, L, hkv, u, g, 0.4 if i % 2 else 0.1)
+                   for i, L in enumerate(lens)])
+    q = queries_for(pattern, n, hq, u, g)
+    v = torch.randn(n, hkv, D, generator=g)
+    q, k, v = (t.to(torch.bfloat16).to(gpu) for t in (q, k, v))
+    attn = Attention.new("mi355x", AttentionSpec(hq, hkv, D, torch.bfloat16, gpu))
+    attn.bind_cache_layout(16)
+    meta = AttentionMetadata(BatchPhase.PREFILL,
+                             cu_seqlens_q=torch.tensor(bounds, dtype=torch.int32, device=gpu),
+                             prefix_lens=torch.zeros(len(lens), dtype=torch.int32, device=gpu),
+                             block_table=torch.zeros(len(lens), 64, dtype=torch.int32,
+                                                     device=gpu))
+    batch = attn.prepare(meta, n)
+    out = batch.forward(q, k, v, BaseAttention())
+    assert bool(torch.isfinite(out).all())
+    want = oatt.prefill_ragged(f32(q), f32(k), f32(v), bounds)
+    assert_close(f32(out).reshape(want.shape), want, f"ragged {pattern} hq={hq}")
+
+
+def _scatter_to_pool(seqs, page, hkv, rng):
+    """Place each [L, hkv, D] sequence on randomly permuted pages of one pool."""
+    pages_per = [(s.shape[0] + page - 1) // page for s in seqs]
+    pool_pages = sum(pages_per) + 1
+    perm = rng.permutation(pool_pages - 1) + 1
+    table = np.zeros((len(seqs), max(pages_per)), dtype=np.int32)
+    pool = torch.zeros(pool_pages, page, hkv, D)
+    off = 0
+    for b, (s, npg) in enumerate(zip(seqs, pages_per)):
+        table[b, :npg] = perm[off: off + npg]
+        off += npg
+        for j in range(npg):
+            chunk = s[j * page: (j + 1) * page]
+            pool[table[b, j], : chunk.shape[0]] = chunk
+    return pool, table
+
+
+@pytest.mark.parametrize("pattern", PATTERNS)
+def test_paged_prefill_extreme_scores(gpu, pattern):
+    """Cached prefix + new tokens: the prefix keys come from the paged pool."""
+    hq, hkv, page = 32, 8, 16
+    g = torch.Generator().manual_seed(len(pattern) * 17)
+    rng = np.random.default_rng(len(pattern))
+    u = _direction(g)
+    prefixes, extends = [900, 130], [64, 200]
+    full = [keys_for(pattern, p + e, hkv, u, g, 0.25) for p, e in zip(prefixes, extends)]
+    vals = [torch.randn(p + e, hkv, D, generator=g) for p, e in zip(prefixes, extends)]
+    kc, table = _scatter_to_pool(full, page, hkv, rng)
+    vc, _ = _scatter_to_pool(vals, page, hkv, np.random.default_rng(len(pattern)))
+    bounds = [0] + np.cumsum(extends).tolist()
+    n = bounds[-1]
+    q = queries_for(pattern, n, hq, u, g)
+    k_new = torch.cat([f[p:] for f, p in zip(full, prefixes)])
+    v_new = torch.cat([x[p:] for x, p in zip(vals, prefixes)])
+    q, k_new, v_new, kc, vc = (t.to(torch.bfloat16).to(gpu) for t in (q, k_new, v_new, kc, vc))
+    attn = Attention.new("mi355x", AttentionSpec(hq, hkv, D, torch.bfloat16, gpu))
+    attn.bind_cache_layout(page)
+    cache = BaseAttention()
+    cache.bind_kv_cache(kc, vc)
+    table_t = torch.from_numpy(table).to(gpu)
+    meta = AttentionMetadata(BatchPhase.PREFILL,
+                             cu_seqlens_q=torch.tensor(bounds, dtype=torch.int32, device=gpu),
+                             prefix_lens=torch.tensor(prefixes, dtype=torch.int32, device=gpu),
+                             block_table=table_t)
+    batch = attn.prepare(meta, n)
+    out = batch.forward(q, k_new, v_new, cache)
+    assert bool(torch.isfinite(out).all())
+    want = oatt.prefill_with_cache(f32(q), f32(kc), f32(vc), table, bounds, prefixes, page)
+    assert_close(f32(out).reshape(want.shape), want, f"paged {pattern}")
+
+
+@pytest.mark.parametrize("pattern", PATTERNS)
+@pytest.mark.parametrize("hq,page", [(16, 1), (32, 16)])
+def test_decode_extreme_scores(gpu, pattern, hq, page):
+    """Vector kernel (group 2, page 1) and matrix-core kernel (group 4, page 16); the long
+    request is split across workgroups, so the split-KV merge meets the extreme maxima too."""
+    hkv = 8
+    g = torch.Generator().manual_seed(len(pattern) * 13 + hq)
+    rng = np.random.default_rng(len(pattern) + hq)
+    u = _direction(g)
+    lens = np.array([1, 700, 9000, 64, 2500], dtype=np.int32)
+    keys = [keys_for(pattern, int(L), hkv, u, g, 0.1 if i % 2 else 0.03)
+            for i, L in enumerate(lens)]
+    vals = [torch.randn(int(L), hkv, D, generator=g) for L in lens]
+    kc, table = _scatter_to_pool(keys, page, hkv, rng)
+    vc, _ = _scatter_to_pool(vals, page, hkv, np.random.default_rng(len(pattern) + hq))
+    q = queries_for(pattern, len(lens), hq, u, g)
+    q, kc, vc = (t.to(torch.bfloat16).to(gpu) for t in (q, kc, vc))
+    attn = Attention.new("mi355x", AttentionSpec(hq, hkv, D, torch.bfloat16, gpu))
+    attn.bind_cache_layout(page)
+    cache = BaseAttention()
+    cache.bind_kv_cache(kc, vc)
+    meta = AttentionMetadata(BatchPhase.DECODE, block_table=torch.from_numpy(table).to(gpu),
+                             cache_seqlens=torch.from_numpy(lens).to(gpu))
+    batch = attn.prepare(meta, len(lens))
+    out = batch.forward(q, q, q, cache)
+    assert bool(torch.isfinite(out).all())
+    want = oatt.decode_with_cache(f32(q), f32(kc), f32(vc), table, lens, page)
+    assert_close(f32(out).reshape(want.shape), want, f"decode {pattern} hq={hq} page={page}")
