@@ -15,8 +15,9 @@
 //             smallest p is the cutoff (the reference's clamp to vocab-1);
 //     a token survives when it passes both, and one token is drawn from the
 //     surviving p renormalised;
-//   * a row whose distribution is invalid (NaN anywhere, or every logit -inf)
-//     yields -1, the reference's invalid-distribution sentinel
+//   * a row whose distribution is invalid (NaN anywhere, every logit -inf, or a scaled
+//     logit of +inf, which makes the reference's softmax NaN) yields -1, the
+//     reference's invalid-distribution sentinel
 //     (sampling_bridge.cpp: output.masked_fill_(!valid, -1)).
 //
 // Algorithm:
@@ -256,7 +257,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a, bool vec
     uint4 rnd = make_uint4(0, 0, 0, 0);
     for_each<DT>(a, row, vec, [&](int64_t i, float x) {
       const float s = scaled(x);
-      if (s != s) nan_seen = true;
+      if (s != s || s == INFINITY) nan_seen = true;
       if (!keep(s) || s == -INFINITY) return;
       const int64_t group = i >> 2;
       if (group != cached_group) {
@@ -298,7 +299,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a, bool vec
   for_each<DT>(a, row, vec, [&](int64_t, float x) {
     const float s = scaled(x);
     if (fast_k && s == s && s != -INFINITY) atomicAdd(&sh.cnt[order_key(s) >> 20], 1u);
-    if (s != s) {
+    if (s != s || s == INFINITY) {  // softmax of a row holding +inf is NaN throughout
       nan_seen = true;
       return;
     }

@@ -121,7 +121,9 @@ def sample_rows(logits: np.ndarray, temperature, top_k, top_p, seed: int, offset
             margins.append(float("inf"))
             continue
         s = scaled_logits(x, t, round_to)
-        if np.isnan(s).any() or not np.isfinite(s).any():
+        # Invalid: NaN anywhere, no finite logit, or a +inf (the reference's softmax of the
+        # scaled row, sampling.rs:261, is NaN throughout once inf - inf appears).
+        if np.isnan(s).any() or np.isposinf(s).any() or not np.isfinite(s).any():
             out[r] = -1
             margins.append(float("inf"))
             continue

@@ -89,6 +89,20 @@ def test_invalid_distribution_sentinel(gpu):
     assert pending.relay().min().item() >= 0
 
 
+def test_positive_infinity_makes_the_row_invalid(gpu):
+    """A scaled logit of +inf makes the reference's softmax NaN throughout (sampling.rs:261):
+    -1 on every filter path (unfiltered race, top-k candidate path, top-p radix path), the raw
+    argmax for greedy rows; fp16 logits overflow to +inf when scaled by a small temperature."""
+    row = [0.0, float("inf"), 1.0, 2.0] + [0.5] * 60
+    logits = torch.tensor([row] * 4, device=gpu)
+    params = [sp(1.0), sp(1.0, 2), sp(1.0, -1, 0.9), sp()]
+    assert Sampler(1).sample_batch_device(logits, params).cpu().tolist() == [-1, -1, -1, 1]
+    half = torch.tensor([[1.0, 30.0, 2.0] + [0.0] * 61] * 3, dtype=torch.float16, device=gpu)
+    params = [sp(1e-4), sp(1e-4, 5), sp(1e-4, -1, 0.5)]
+    assert Sampler(1).sample_batch_device(half, params).cpu().tolist() == [-1, -1, -1]
+    assert Sampler(1).sample_batch_device(half, [sp(0.5, 5)] * 3).min().item() >= 0
+
+
 def test_parameter_count_mismatch(gpu):
     with pytest.raises(SamplingError):
         Sampler(0).sample_batch(torch.zeros(2, 3, device=gpu), [sp()])

@@ -129,6 +129,27 @@ def test_invalid_rows_give_sentinel():
     assert ids.tolist() == [-1, -1]
 
 
+def test_positive_infinity_makes_the_row_invalid():
+    """The reference softmaxes the scaled row in torch (sampling.rs:261): a +inf entry gives
+    inf - inf = NaN, so the whole distribution is NaN and the row is invalid (-1) for every
+    filter; greedy rows take the raw argmax and are unaffected. An fp16 row scaled by a small
+    temperature overflows to +inf the same way."""
+    import torch
+    row = torch.tensor([[0.0, float("inf"), 1.0, 2.0]])
+    assert bool(torch.isnan(torch.softmax(row, -1)).all())
+    half = torch.tensor([[1.0, 30.0, 2.0]], dtype=torch.float16)
+    assert bool(torch.isinf(half / 1e-4).any())  # 3e5 > fp16 max
+    logits = np.array([[0.0, np.inf, 1.0, 2.0]] * 4, np.float32)
+    ids, _ = osamp.sample_rows(logits, [1.0, 1.0, 1.0, 0.0], [-1, 2, -1, -1], [1.0, 1.0, 0.9, 1.0],
+                               0, 0)
+    assert ids.tolist() == [-1, -1, -1, 1]
+    h = np.array([[1.0, 30.0, 2.0]], np.float32)
+    with np.errstate(over="ignore"):  # the fp16 cast overflows on purpose
+        ids, _ = osamp.sample_rows(h, [1e-4], [-1], [1.0], 0, 0,
+                                   lambda v: v.astype(np.float16).astype(np.float32))
+    assert ids.tolist() == [-1]
+
+
 # --------------------------------------------------------------------------- RoPE
 def test_rope_reference_fixture_eager_formula():
     # ops.rs:498-530: q = arange(32).view(4,2,4), k = arange(16).view(4,1,4), positions
