@@ -175,7 +175,8 @@ def _edge_rows(case, vocab, g):
     return x * 3
 
 
-@pytest.mark.parametrize("dtype,name", [(torch.bfloat16, "bf16"), (torch.float32, None)])
+@pytest.mark.parametrize("dtype,name", [(torch.bfloat16, "bf16"), (torch.float16, "f16"),
+                                        (torch.float32, None)])
 @pytest.mark.parametrize("case,k,p", [
     ("ties", 50, 0.9), ("ties", 1, 1.0), ("ties_fit", 50, 0.9), ("ties_fit", 3000, 0.95),
     ("plain", 2000, 0.95), ("plain", 2048, 1.0), ("plain", 2049, 0.99), ("plain", 4000, 0.9),
