@@ -179,3 +179,37 @@ def test_decode_extreme_scores(gpu, pattern, hq, page):
     assert bool(torch.isfinite(out).all())
     want = oatt.decode_with_cache(f32(q), f32(kc), f32(vc), table, lens, page)
     assert_close(f32(out).reshape(want.shape), want, f"decode {pattern} hq={hq} page={page}")
+
+
+@pytest.mark.parametrize("pattern", PATTERNS)
+def test_split_prefill_extreme_scores(gpu, pattern):
+    """A long cached prefix under a few new tokens: the plan cuts the item along its keys and a
+    second launch merges the chunks by log-sum-exp, so chunks whose maxima differ by hundreds
+    of units (or lie wholly below -500) must combine exactly."""
+    hq, hkv, page = 32, 8, 16
+    g = torch.Generator().manual_seed(len(pattern) * 5 + 1)
+    rng = np.random.default_rng(len(pattern) + 11)
+    u = _direction(g)
+    prefixes, extends = [6000], [40]
+    full = [keys_for(pattern, prefixes[0] + extends[0], hkv, u, g, 0.05)]
+    vals = [torch.randn(prefixes[0] + extends[0], hkv, D, generator=g)]
+    kc, table = _scatter_to_pool(full, page, hkv, rng)
+    vc, _ = _scatter_to_pool(vals, page, hkv, np.random.default_rng(len(pattern) + 11))
+    bounds = [0, extends[0]]
+    q = queries_for(pattern, extends[0], hq, u, g)
+    k_new, v_new = full[0][prefixes[0]:], vals[0][prefixes[0]:]
+    q, k_new, v_new, kc, vc = (t.to(torch.bfloat16).to(gpu) for t in (q, k_new, v_new, kc, vc))
+    attn = Attention.new("mi355x", AttentionSpec(hq, hkv, D, torch.bfloat16, gpu))
+    attn.bind_cache_layout(page)
+    cache = BaseAttention()
+    cache.bind_kv_cache(kc, vc)
+    meta = AttentionMetadata(BatchPhase.PREFILL,
+                             cu_seqlens_q=torch.tensor(bounds, dtype=torch.int32, device=gpu),
+                             prefix_lens=torch.tensor(prefixes, dtype=torch.int32, device=gpu),
+                             block_table=torch.from_numpy(table).to(gpu))
+    batch = attn.prepare(meta, extends[0])
+    assert batch.plan.plan.info()["split_items"] > 0
+    out = batch.forward(q, k_new, v_new, cache)
+    assert bool(torch.isfinite(out).all())
+    want = oatt.prefill_with_cache(f32(q), f32(kc), f32(vc), table, bounds, prefixes, page)
+    assert_close(f32(out).reshape(want.shape), want, f"split prefill {pattern}")
