@@ -173,3 +173,49 @@ def test_qk_norm_many_rows_with_a_ragged_tail(gpu, dtype):
     check(q, want_q, dtype, TOL[dtype][0])
     check(k, want_k, dtype, TOL[dtype][0])
     assert torch.equal(packed[:, 3072:], vb)
+
+
+def check_rel(actual, expected_f32, dtype, tol):
+    """`check` with the absolute bound widened to one unit in the last place of large outputs
+    (the spike row normalises to ~64, where a bf16 ulp is 0.5)."""
+    want = obf.round_to(expected_f32, NAME[dtype])
+    got = f32(actual)
+    ulp = 2.0 ** (-7 if dtype == torch.bfloat16 else -10)
+    bound = np.maximum(tol, ulp * np.abs(want))
+    assert (np.abs(got - want) <= bound).all(), float((np.abs(got - want) - bound).max())
+    assert cos(got, expected_f32) > 0.9999
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_norms_on_pathological_rows(gpu, dtype):
+    """All-zero rows (rsqrt(eps) times 0 = 0), one large element among small ones (the sum of
+    squares must not lose the small ones' share of the output), large magnitudes (bf16 / fp16
+    values near 200, squares summed in fp32) and tiny magnitudes (values ~1e-3, where eps
+    dominates): RMSNorm, add-RMSNorm and QK-norm against the fp32 oracle."""
+    g = torch.Generator().manual_seed(77)
+    width = 4096
+    rows = [torch.zeros(width), torch.randn(width, generator=g) * 1e-3,
+            torch.randn(width, generator=g) * 200]
+    spike = torch.randn(width, generator=g) * 0.01
+    spike[1234] = 150.0
+    rows.append(spike)
+    x = torch.stack(rows).to(dtype).to(gpu)
+    w = torch.empty(width).uniform_(0.5, 1.5, generator=g).to(dtype).to(gpu)
+    out = ops.rms_norm(x, w, 1e-6)
+    assert bool(torch.isfinite(out).all()) and bool((out[0] == 0).all())
+    check_rel(out, onorm.rms_norm_f32(f32(x), f32(w), 1e-6), dtype, TOL[dtype][0])
+    r = torch.flip(x, [0]).contiguous()
+    want_out, want_sum = onorm.add_rms_norm_f32(f32(x), f32(r), f32(w), 1e-6)
+    out, summed = ops.add_rms_norm(x.clone(), r, w, 1e-6)
+    np.testing.assert_array_equal(f32(summed), obf.round_to(want_sum, NAME[dtype]))
+    check_rel(out, want_out, dtype, TOL[dtype][1])
+    # QK-norm: the same rows as heads of width 128 (zero heads, spike heads, tiny heads)
+    q = x.view(4, 32, 128).clone()
+    k = x.view(4, 32, 128)[:, :8].clone()
+    qw = w[:128].contiguous()
+    kw = w[128:256].contiguous()
+    want_q = onorm.rms_norm_f32(f32(q).reshape(-1, 128), f32(qw), 1e-6)
+    want_k = onorm.rms_norm_f32(f32(k).reshape(-1, 128), f32(kw), 1e-6)
+    ops.qk_norm(q, k, qw, kw, 1e-6)
+    check_rel(q.reshape(-1, 128), want_q, dtype, TOL[dtype][0])
+    check_rel(k.reshape(-1, 128), want_k, dtype, TOL[dtype][0])
